@@ -1,0 +1,285 @@
+"""FlowEdge Diffusion Policy engine on AMD Instinct MI355X.
+
+``Engine`` mirrors the reference's ``flowedge.Engine`` binding (``python/flowedge_ext.cc:518-561,
+791-847``) for the Diffusion Policy path: same constructor, properties and method names, numpy in
+and out, errors raised as ``RuntimeError`` with ``fe_engine_last_error()``.  Every call goes
+through the C ABI in ``include/flowedge.h`` (``libflowedge_amd.so``); there is no host fallback:
+if the library is not built, importing the binding fails.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import checkpoint  # noqa: F401  (re-exported helpers)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libflowedge_amd.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_lib = None
+
+EXPORTS = [
+    "fe_engine_last_error", "fe_engine_load", "fe_engine_load_with_threads", "fe_weights_load",
+    "fe_weights_size_bytes", "fe_weights_free", "fe_engine_create_from_weights",
+    "fe_engine_create_from_weights_auto", "fe_engine_thread_count", "fe_engine_cuda_resident",
+    "fe_engine_model_metadata", "fe_engine_action_dim", "fe_engine_action_horizon",
+    "fe_engine_diffusion_metadata", "fe_engine_condition_dim", "fe_engine_sample_diffusion",
+    "fe_engine_diffusion_denoise", "fe_engine_sample_condition", "fe_engine_free",
+    "fe_engine_sample_diffusion_batch", "fe_engine_sample_condition_batch",
+    "fe_engine_diffusion_denoise_batch", "fe_engine_sample_device", "fe_engine_prepare",
+    "fe_engine_max_batch", "fe_engine_device_bytes", "fe_device_alloc_count",
+    "fe_engine_last_device_ms",
+]
+
+SCHEDULERS = {"ddim": 0, "ddpm": 1}
+SOLVERS = {"euler": 0, "heun": 1, "rk4": 2}
+
+
+class DiffusionMetadata(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("protocol_version", ctypes.c_uint32),
+                ("clip_sample", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("action_dim", ctypes.c_uint64), ("condition_dim", ctypes.c_uint64),
+                ("horizon", ctypes.c_uint64), ("action_steps", ctypes.c_uint64),
+                ("observation_steps", ctypes.c_uint64), ("train_timesteps", ctypes.c_uint64),
+                ("clip_sample_range", ctypes.c_float), ("reserved_float", ctypes.c_float)]
+
+
+class ModelMetadata(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("protocol_version", ctypes.c_uint32),
+                ("architecture", ctypes.c_uint32), ("precision", ctypes.c_uint32),
+                ("model_digest", ctypes.c_uint8 * 16), ("d_model", ctypes.c_uint64),
+                ("n_layers", ctypes.c_uint64), ("d_inner", ctypes.c_uint64),
+                ("d_state", ctypes.c_uint64), ("d_conv", ctypes.c_uint64),
+                ("action_dim", ctypes.c_uint64), ("condition_dim", ctypes.c_uint64),
+                ("decode_snapshot_bytes", ctypes.c_uint64)]
+
+
+def lib():
+    """The loaded C ABI library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() or "
+                          "python -m flowedge_amd.build")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, sz, u64, cint = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int
+    L.fe_engine_last_error.restype = ctypes.c_char_p
+    for name in ("fe_engine_load",):
+        getattr(L, name).restype = vp
+        getattr(L, name).argtypes = [ctypes.c_char_p]
+    L.fe_engine_load_with_threads.restype = vp
+    L.fe_engine_load_with_threads.argtypes = [ctypes.c_char_p, ctypes.c_uint]
+    L.fe_weights_load.restype = vp
+    L.fe_weights_load.argtypes = [ctypes.c_char_p]
+    L.fe_weights_size_bytes.restype = sz
+    L.fe_weights_size_bytes.argtypes = [vp]
+    L.fe_weights_free.argtypes = [vp]
+    L.fe_engine_create_from_weights.restype = vp
+    L.fe_engine_create_from_weights.argtypes = [vp, ctypes.c_uint]
+    L.fe_engine_create_from_weights_auto.restype = vp
+    L.fe_engine_create_from_weights_auto.argtypes = [vp]
+    L.fe_engine_free.argtypes = [vp]
+    L.fe_engine_thread_count.restype = ctypes.c_uint
+    L.fe_engine_thread_count.argtypes = [vp]
+    L.fe_engine_cuda_resident.argtypes = [vp]
+    L.fe_engine_model_metadata.argtypes = [vp, ctypes.POINTER(ModelMetadata)]
+    for name in ("fe_engine_action_dim", "fe_engine_action_horizon", "fe_engine_condition_dim",
+                 "fe_engine_max_batch", "fe_engine_device_bytes"):
+        getattr(L, name).restype = sz
+        getattr(L, name).argtypes = [vp]
+    L.fe_engine_diffusion_metadata.argtypes = [vp, ctypes.POINTER(DiffusionMetadata)]
+    L.fe_engine_sample_diffusion.argtypes = [vp, _f32p, _f32p, sz, cint, u64, _f32p]
+    L.fe_engine_diffusion_denoise.argtypes = [vp, _f32p, _f32p, ctypes.c_float, _f32p]
+    L.fe_engine_sample_condition.argtypes = [vp, _f32p, _f32p, sz, cint, _f32p]
+    L.fe_engine_sample_diffusion_batch.argtypes = [vp, _f32p, _f32p, sz, sz, cint, u64, _f32p]
+    L.fe_engine_sample_condition_batch.argtypes = [vp, _f32p, _f32p, sz, sz, cint, _f32p]
+    L.fe_engine_diffusion_denoise_batch.argtypes = [vp, _f32p, _f32p, sz, ctypes.c_float, _f32p]
+    L.fe_engine_sample_device.argtypes = [vp, cint, vp, vp, sz, sz, cint, u64, vp]
+    L.fe_engine_prepare.argtypes = [vp, cint, sz, sz, cint]
+    L.fe_device_alloc_count.restype = u64
+    L.fe_engine_last_device_ms.restype = ctypes.c_float
+    L.fe_engine_last_device_ms.argtypes = [vp]
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return lib().fe_engine_last_error().decode()
+
+
+def device_alloc_count() -> int:
+    return int(lib().fe_device_alloc_count())
+
+
+def _arr(a, shape=None) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if shape is not None and a.size != int(np.prod(shape)):
+        raise RuntimeError(f"expected {int(np.prod(shape))} values, got {a.size}")
+    return a
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+class Engine:
+    """One loaded Diffusion Policy checkpoint, device-resident on the current GPU."""
+
+    def __init__(self, path: str, threads: int | None = None):
+        L = lib()
+        h = (L.fe_engine_load(path.encode()) if threads is None else
+             L.fe_engine_load_with_threads(path.encode(), int(threads)))
+        if not h:
+            raise RuntimeError(last_error())
+        self._h = h
+        md = DiffusionMetadata()
+        if L.fe_engine_diffusion_metadata(self._h, ctypes.byref(md)) != 0:
+            raise RuntimeError(last_error())
+        self._md = md
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().fe_engine_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- properties (flowedge_ext.cc:793-800) ----
+    @property
+    def action_dim(self) -> int:
+        return int(lib().fe_engine_action_dim(self._h))
+
+    @property
+    def action_horizon(self) -> int:
+        return int(lib().fe_engine_action_horizon(self._h))
+
+    @property
+    def condition_dim(self) -> int:
+        return int(lib().fe_engine_condition_dim(self._h))
+
+    @property
+    def thread_count(self) -> int:
+        return int(lib().fe_engine_thread_count(self._h))
+
+    @property
+    def cuda_resident(self) -> bool:
+        return bool(lib().fe_engine_cuda_resident(self._h))
+
+    @property
+    def diffusion_metadata(self) -> dict:
+        md = self._md
+        return {f: getattr(md, f) for f, _ in DiffusionMetadata._fields_ if "reserved" not in f}
+
+    @property
+    def model_metadata(self) -> dict:
+        mm = ModelMetadata()
+        if lib().fe_engine_model_metadata(self._h, ctypes.byref(mm)) != 0:
+            raise RuntimeError(last_error())
+        return {"architecture": mm.architecture, "precision": mm.precision,
+                "action_dim": mm.action_dim, "condition_dim": mm.condition_dim}
+
+    @property
+    def max_batch(self) -> int:
+        return int(lib().fe_engine_max_batch(self._h))
+
+    @property
+    def device_bytes(self) -> int:
+        return int(lib().fe_engine_device_bytes(self._h))
+
+    @property
+    def last_device_ms(self) -> float:
+        return float(lib().fe_engine_last_device_ms(self._h))
+
+    def _values(self) -> int:
+        return self.action_horizon * self.action_dim
+
+    def _check(self, rc: int):
+        if rc != 0:
+            raise RuntimeError(last_error())
+
+    # ---- Diffusion Policy (flowedge_ext.cc:518-561, 837-847) ----
+    def sample_diffusion(self, condition, noise, steps: int = 10, scheduler: str = "ddim",
+                         seed: int = 0) -> np.ndarray:
+        out = np.empty((self.action_horizon, self.action_dim), np.float32)
+        self.sample_diffusion_into(condition, noise, out, steps, scheduler, seed)
+        return out
+
+    def sample_diffusion_into(self, condition, noise, output, steps: int = 10,
+                              scheduler: str = "ddim", seed: int = 0) -> None:
+        c = _arr(condition, (self.condition_dim,))
+        n = _arr(noise, (self._values(),))
+        if not (isinstance(output, np.ndarray) and output.dtype == np.float32 and
+                output.flags["C_CONTIGUOUS"] and output.size == self._values()):
+            raise RuntimeError("output must be a contiguous float32 array of horizon*action_dim")
+        if scheduler not in SCHEDULERS:
+            raise RuntimeError("scheduler must be 'ddim' or 'ddpm'")
+        self._check(lib().fe_engine_sample_diffusion(self._h, _p(c), _p(n), steps,
+                                                     SCHEDULERS[scheduler], seed, _p(output)))
+
+    def diffusion_denoise(self, condition, sample, timestep: float) -> np.ndarray:
+        c = _arr(condition, (self.condition_dim,))
+        s = _arr(sample, (self._values(),))
+        out = np.empty((self.action_horizon, self.action_dim), np.float32)
+        self._check(lib().fe_engine_diffusion_denoise(self._h, _p(c), _p(s), float(timestep),
+                                                      _p(out)))
+        return out
+
+    def sample_condition(self, condition, noise, output, steps: int = 10,
+                         method: str = "euler") -> None:
+        c = _arr(condition, (self.condition_dim,))
+        n = _arr(noise, (self._values(),))
+        if method not in SOLVERS:
+            raise RuntimeError("method must be 'euler', 'heun' or 'rk4'")
+        self._check(lib().fe_engine_sample_condition(self._h, _p(c), _p(n), steps,
+                                                     SOLVERS[method], _p(output)))
+
+    # ---- batched extensions ----
+    def sample_diffusion_batch(self, condition, noise, steps: int = 10, scheduler: str = "ddim",
+                               seed: int = 0) -> np.ndarray:
+        c = _arr(condition)
+        b = c.size // self.condition_dim
+        n = _arr(noise, (b * self._values(),))
+        out = np.empty((b, self.action_horizon, self.action_dim), np.float32)
+        self._check(lib().fe_engine_sample_diffusion_batch(self._h, _p(c), _p(n), b, steps,
+                                                           SCHEDULERS[scheduler], seed, _p(out)))
+        return out
+
+    def sample_condition_batch(self, condition, noise, steps: int = 10,
+                               method: str = "euler") -> np.ndarray:
+        c = _arr(condition)
+        b = c.size // self.condition_dim
+        n = _arr(noise, (b * self._values(),))
+        out = np.empty((b, self.action_horizon, self.action_dim), np.float32)
+        self._check(lib().fe_engine_sample_condition_batch(self._h, _p(c), _p(n), b, steps,
+                                                           SOLVERS[method], _p(out)))
+        return out
+
+    def diffusion_denoise_batch(self, condition, sample, timestep: float) -> np.ndarray:
+        c = _arr(condition)
+        b = c.size // self.condition_dim
+        s = _arr(sample, (b * self._values(),))
+        out = np.empty((b, self.action_horizon, self.action_dim), np.float32)
+        self._check(lib().fe_engine_diffusion_denoise_batch(self._h, _p(c), _p(s), b,
+                                                            float(timestep), _p(out)))
+        return out
+
+    def sample_device(self, kind: int, cond_ptr: int, noise_ptr: int, batch: int, steps: int,
+                      mode: int, seed: int, action_ptr: int) -> None:
+        """Device-resident sampling: the pointers are device addresses (e.g. tensor.data_ptr())."""
+        self._check(lib().fe_engine_sample_device(self._h, kind, cond_ptr, noise_ptr, batch,
+                                                  steps, mode, seed, action_ptr))
+
+    def prepare(self, kind: int, batch: int, steps: int, mode: int) -> None:
+        self._check(lib().fe_engine_prepare(self._h, kind, batch, steps, mode))

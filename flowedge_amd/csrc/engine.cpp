@@ -1,0 +1,1383 @@
+// Host runtime and C ABI of the MI355X Diffusion Policy engine.
+//
+// Mirrors the reference's split (src/core/api/engine.cc -> runtime/engine_runtime.cc ->
+// heads/diffusion/diffusion.cc) for the Diffusion Policy path:
+//   * load: mmap the dp.* checkpoint, validate dp.meta exactly as diffusion.cc:391-427 does
+//     (plus prediction type 1 = velocity for the flow-ODE U-Net), plan ONE device arena for
+//     repacked weights, FiLM tables, activations of `max_batch` samples and I/O buffers, then a
+//     single hipMalloc and the uploads;
+//   * sample: host -> pinned staging -> H2D, one hipGraph replay of the whole sampling loop (all
+//     U-Net evaluations plus the DDIM/DDPM/ODE updates), D2H -> host.  A graph is captured once per
+//     (kind, batch, steps, mode) and cached; replays allocate nothing.
+//   * errors: int status codes and a thread-local message as engine.cc:22-26, 507-540.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <list>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/flowedge.h"
+#include "kernels.h"
+#include "safetensors.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// Thread-local last error (engine.cc:22-26): reset to "" at each ABI entry.
+// ---------------------------------------------------------------------------------------------
+thread_local const char* t_error = "";
+thread_local std::string t_error_buf;
+
+void set_error(const char* msg) { t_error = msg; }
+void set_error(const std::string& msg) {
+  t_error_buf = msg;
+  t_error = t_error_buf.c_str();
+}
+void clear_error() { t_error = ""; }
+
+std::atomic<std::uint64_t> g_device_allocs{0};
+
+bool env_flag(const char* name) {
+  const char* v = std::getenv(name);
+  return v != nullptr && v[0] == '1' && v[1] == '\0';
+}
+
+constexpr unsigned kMaxPoolThreads = 8;  // engine_runtime.h:39
+constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
+constexpr std::size_t kFinalNormGroups = 8;  // diffusion.cc:28
+constexpr std::size_t kAlign = 256;
+
+// ---------------------------------------------------------------------------------------------
+// Configuration (diffusion.h:19-33 / diffusion.cc:391-427).
+// ---------------------------------------------------------------------------------------------
+struct Config {
+  std::size_t action_dim = 0, horizon = 0, action_steps = 0, obs_steps = 0, cond_dim = 0,
+              stages = 0, kernel = 0, groups = 0, tdim = 0, train_timesteps = 0;
+  std::size_t prediction = 0;  // 0 epsilon, 1 velocity
+  bool clip = false;
+  float clip_range = 1.0f;
+  std::size_t dims[kMaxStages] = {};
+};
+
+bool size_value(float v, std::size_t& out) {
+  if (!std::isfinite(v) || v < 0.0f || std::floor(v) != v || v > 4294967295.0f) return false;
+  out = static_cast<std::size_t>(v);
+  return true;
+}
+
+bool f32_vector(const fe::TensorInfo* t, std::size_t n) {
+  return t != nullptr && !t->bf16 && t->shape.size() == 1 && t->shape[0] == n;
+}
+
+bool parse_config(const fe::Checkpoint& ck, Config& c, std::string& err) {
+  const fe::TensorInfo* meta = ck.find("dp.meta");
+  const fe::TensorInfo* dims = ck.find("dp.dims");
+  if (!f32_vector(meta, 16) || dims == nullptr || dims->bf16 || dims->shape.size() != 1) {
+    err = "Checkpoint has no valid Diffusion Policy head (dp.meta / dp.dims)";
+    return false;
+  }
+  const float* m = static_cast<const float*>(meta->data);
+  std::size_t schema, beta, norm, clip;
+  const bool ok =
+      size_value(m[0], schema) && size_value(m[1], c.action_dim) && size_value(m[2], c.horizon) &&
+      size_value(m[3], c.action_steps) && size_value(m[4], c.obs_steps) &&
+      size_value(m[5], c.cond_dim) && size_value(m[6], c.stages) && size_value(m[7], c.kernel) &&
+      size_value(m[8], c.groups) && size_value(m[9], c.tdim) &&
+      size_value(m[10], c.train_timesteps) && size_value(m[11], beta) &&
+      size_value(m[12], c.prediction) && size_value(m[13], clip) && size_value(m[15], norm) &&
+      schema == 1 && beta == 0 && c.prediction <= 1 && norm == 0 && clip <= 1 &&
+      c.action_dim > 0 && c.horizon > 0 && c.action_steps > 0 && c.obs_steps > 0 &&
+      c.obs_steps <= c.horizon && c.action_steps <= c.horizon - c.obs_steps + 1 &&
+      c.cond_dim > 0 && c.stages >= 2 && c.stages <= kMaxStages && c.kernel > 0 &&
+      c.kernel % 2 == 1 && c.groups > 0 && c.tdim >= 4 && c.tdim % 2 == 0 &&
+      c.train_timesteps > 0 && dims->shape[0] == c.stages && std::isfinite(m[14]) && m[14] > 0.0f;
+  if (!ok) {
+    err = "Invalid dp.meta";
+    return false;
+  }
+  c.clip = clip != 0;
+  c.clip_range = m[14];
+  const float* d = static_cast<const float*>(dims->data);
+  for (std::size_t s = 0; s < c.stages; ++s)
+    if (!size_value(d[s], c.dims[s]) || c.dims[s] == 0 || c.dims[s] % c.groups != 0) {
+      err = "Invalid dp.dims";
+      return false;
+    }
+  if (c.dims[0] % kFinalNormGroups != 0 || c.horizon % (std::size_t{1} << (c.stages - 1)) != 0) {
+    err = "Invalid U-Net widths or horizon";
+    return false;
+  }
+  return true;
+}
+
+// Device kernels are specialised for these shapes; anything else is rejected at load.
+bool supported_shape(const Config& c, std::string& err) {
+  if (c.kernel != 3 && c.kernel != 5) {
+    err = "Unsupported U-Net kernel size (3 and 5 are supported)";
+    return false;
+  }
+  const std::size_t h = c.horizon;
+  if (h > 32 || (h & (h - 1)) != 0) {
+    err = "Unsupported horizon (powers of two up to 32 are supported)";
+    return false;
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Arena planning: every buffer is an offset into one allocation.
+// ---------------------------------------------------------------------------------------------
+struct Plan {
+  std::size_t size = 0;
+  std::size_t take(std::size_t bytes) {
+    const std::size_t off = (size + kAlign - 1) / kAlign * kAlign;
+    size = off + bytes;
+    return off;
+  }
+};
+
+struct ConvSlot {
+  fe::hip::ConvOp op;
+  std::size_t w_off = 0, b_off = 0;
+  const fe::TensorInfo* w_src = nullptr;
+  const fe::TensorInfo* b_src = nullptr;
+  bool transpose_storage = false;  // ConvTranspose1d [IC][OC][K]
+};
+
+struct NormSlot {
+  std::size_t g_off = 0, b_off = 0;
+  const fe::TensorInfo* g_src = nullptr;
+  const fe::TensorInfo* b_src = nullptr;
+};
+
+struct Block {
+  ConvSlot c1, c2, res;
+  NormSlot n1, n2;
+  bool identity = false;
+  std::size_t ic = 0, oc = 0, len = 0;
+  std::size_t film_off = 0;             // row offset of this block's 2*oc FiLM outputs
+  const fe::TensorInfo* film_w = nullptr;
+  const fe::TensorInfo* film_b = nullptr;
+  std::size_t h1_off = 0, h2_off = 0, r_off = 0;  // activations [B][oc][len]
+  // Output view: base offset and per-sample stride (floats).
+  std::size_t out_off = 0;
+  std::size_t out_stride = 0;
+};
+
+struct GraphEntry {
+  int kind = 0, mode = 0;
+  std::size_t batch = 0, steps = 0;
+  hipGraphExec_t exec = nullptr;
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// Engine.
+// ---------------------------------------------------------------------------------------------
+struct FeWeights {
+  std::shared_ptr<const fe::Checkpoint> ck;
+};
+
+struct FeEngine {
+  Config cfg;
+  unsigned threads = 0;
+  int device = 0;
+  std::size_t max_batch = 0;
+  std::size_t values = 0;  // H * A
+  bool bf16_convs = false, any_bf16 = false;
+
+  // Arena.
+  char* arena = nullptr;
+  std::size_t arena_bytes = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  float last_ms = -1.0f;
+  bool timed = false;
+
+  // Host pinned staging.
+  float* pin_cond = nullptr;
+  float* pin_noise = nullptr;
+  float* pin_action = nullptr;
+  std::uint64_t* pin_seed = nullptr;
+
+  // Layout.
+  std::size_t te1w = 0, te1b = 0, te2w = 0, te2b = 0;
+  std::size_t film_wt = 0, film_wc = 0, film_bias = 0, film_total = 0;
+  std::size_t amin = 0, amax = 0;
+  Block down[kMaxStages][2];
+  ConvSlot ds[kMaxStages];
+  std::size_t ds_out[kMaxStages] = {};
+  Block mid[2];
+  Block up[kMaxStages][2];
+  ConvSlot us[kMaxStages];
+  std::size_t concat[kMaxStages] = {};  // up stage u concat buffer [B][2*high][len]
+  std::size_t fconv_out = 0;
+  ConvSlot fconv, fout;
+  NormSlot fnorm;
+  std::size_t max_nfe = 0;
+  std::size_t time_m = 0, film_table = 0, film_cond = 0;
+  std::size_t x_state = 0, x_in = 0, k_stages = 0;
+  std::size_t in_cond = 0, in_noise = 0, out_action = 0, seed_dev = 0;
+  std::size_t up_in[kMaxStages] = {};   // input of up stage u (its concat buffer)
+  std::size_t final_in = 0;
+
+  std::list<GraphEntry> graphs;  // most recently used first
+
+  template <typename T = float>
+  T* ptr(std::size_t off) const {
+    return reinterpret_cast<T*>(arena + off);
+  }
+
+  ~FeEngine() {
+    for (auto& g : graphs)
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (ev0) (void)hipEventDestroy(ev0);
+    if (ev1) (void)hipEventDestroy(ev1);
+    if (stream) (void)hipStreamDestroy(stream);
+    if (arena) (void)hipFree(arena);
+    if (pin_cond) (void)hipHostFree(pin_cond);
+  }
+};
+
+namespace {
+
+constexpr std::size_t kGraphCache = 32;
+
+// Sizing and validation of the weights; fills the slots and offsets.
+struct Builder {
+  FeEngine& e;
+  const fe::Checkpoint& ck;
+  Plan plan;
+  std::string err;
+
+  bool conv(const std::string& p, std::size_t oc, std::size_t ic, std::size_t k, int mode,
+            ConvSlot& s, bool transpose_storage = false) {
+    const fe::TensorInfo* w = ck.find(p + ".w");
+    const fe::TensorInfo* b = ck.find(p + ".b");
+    if (w == nullptr || w->shape.size() != 3 || w->shape[0] != (transpose_storage ? ic : oc) ||
+        w->shape[1] != (transpose_storage ? oc : ic) || w->shape[2] != k || !f32_vector(b, oc)) {
+      err = "Missing or malformed convolution " + p;
+      return false;
+    }
+    s.w_src = w;
+    s.b_src = b;
+    s.transpose_storage = transpose_storage;
+    s.op.bf16 = w->bf16;
+    s.op.mode = mode;
+    s.op.k = static_cast<int>(k);
+    s.op.ic = static_cast<int>(ic);
+    s.op.oc = static_cast<int>(oc);
+    s.w_off = plan.take(w->elements() * (w->bf16 ? 2 : 4));
+    s.b_off = plan.take(oc * 4);
+    if (w->bf16) e.bf16_convs = true, e.any_bf16 = true;
+    return true;
+  }
+
+  bool norm(const std::string& p, std::size_t c, NormSlot& n) {
+    n.g_src = ck.find(p + ".w");
+    n.b_src = ck.find(p + ".b");
+    if (!f32_vector(n.g_src, c) || !f32_vector(n.b_src, c)) {
+      err = "Missing or malformed GroupNorm " + p;
+      return false;
+    }
+    n.g_off = plan.take(c * 4);
+    n.b_off = plan.take(c * 4);
+    return true;
+  }
+
+  bool linear_shape(const std::string& p, std::size_t out, std::size_t in,
+                    const fe::TensorInfo*& w, const fe::TensorInfo*& b) {
+    w = ck.find(p + ".w");
+    b = ck.find(p + ".b");
+    if (w == nullptr || w->shape.size() != 2 || w->shape[0] != out || w->shape[1] != in ||
+        !f32_vector(b, out)) {
+      err = "Missing or malformed linear " + p;
+      return false;
+    }
+    if (w->bf16) e.any_bf16 = true;
+    return true;
+  }
+
+  bool block(const std::string& p, std::size_t ic, std::size_t oc, std::size_t len, Block& blk) {
+    const Config& c = e.cfg;
+    blk.ic = ic;
+    blk.oc = oc;
+    blk.len = len;
+    blk.identity = ic == oc;
+    if (!conv(p + ".c1", oc, ic, c.kernel, fe::hip::kConvSame, blk.c1) ||
+        !norm(p + ".n1", oc, blk.n1) ||
+        !linear_shape(p + ".film", 2 * oc, c.tdim + c.cond_dim, blk.film_w, blk.film_b) ||
+        !conv(p + ".c2", oc, oc, c.kernel, fe::hip::kConvSame, blk.c2) ||
+        !norm(p + ".n2", oc, blk.n2))
+      return false;
+    if (!blk.identity && !conv(p + ".res", oc, ic, 1, fe::hip::kConvSame, blk.res)) return false;
+    blk.film_off = e.film_total;
+    e.film_total += 2 * oc;
+    for (ConvSlot* s : {&blk.c1, &blk.c2, &blk.res}) {
+      s->op.lin = static_cast<int>(len);
+      s->op.lout = static_cast<int>(len);
+    }
+    return true;
+  }
+
+  bool build() {
+    Config& c = e.cfg;
+    const std::size_t B = e.max_batch;
+    const fe::TensorInfo *w, *b;
+    if (!linear_shape("dp.te1", 4 * c.tdim, c.tdim, w, b)) return false;
+    e.te1w = plan.take(w->elements() * 4);
+    e.te1b = plan.take(b->elements() * 4);
+    if (!linear_shape("dp.te2", c.tdim, 4 * c.tdim, w, b)) return false;
+    e.te2w = plan.take(w->elements() * 4);
+    e.te2b = plan.take(b->elements() * 4);
+    const fe::TensorInfo* amin = ck.find("dp.action_min");
+    const fe::TensorInfo* amax = ck.find("dp.action_max");
+    if (!f32_vector(amin, c.action_dim) || !f32_vector(amax, c.action_dim)) {
+      err = "Missing or malformed action range";
+      return false;
+    }
+    const float* mn = static_cast<const float*>(amin->data);
+    const float* mx = static_cast<const float*>(amax->data);
+    for (std::size_t i = 0; i < c.action_dim; ++i)
+      if (!std::isfinite(mn[i]) || !std::isfinite(mx[i]) || mx[i] <= mn[i]) {
+        err = "Invalid action range";
+        return false;
+      }
+    e.amin = plan.take(c.action_dim * 4);
+    e.amax = plan.take(c.action_dim * 4);
+
+    // Down path.
+    std::size_t len = c.horizon;
+    for (std::size_t s = 0; s < c.stages; ++s) {
+      const std::size_t ic = s == 0 ? c.action_dim : c.dims[s - 1];
+      const std::string p = "dp.d" + std::to_string(s);
+      if (!block(p + ".r0", ic, c.dims[s], len, e.down[s][0]) ||
+          !block(p + ".r1", c.dims[s], c.dims[s], len, e.down[s][1]))
+        return false;
+      if (s + 1 < c.stages) {
+        if (!conv(p + ".ds", c.dims[s], c.dims[s], 3, fe::hip::kConvDown, e.ds[s])) return false;
+        e.ds[s].op.lin = static_cast<int>(len);
+        e.ds[s].op.lout = static_cast<int>(len / 2);
+        len /= 2;
+      }
+    }
+    const std::size_t bottom = c.dims[c.stages - 1];
+    for (int m = 0; m < 2; ++m)
+      if (!block("dp.m" + std::to_string(m), bottom, bottom, len, e.mid[m])) return false;
+    for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+      const std::size_t high = c.dims[c.stages - 1 - u], low = c.dims[c.stages - 2 - u];
+      const std::string p = "dp.u" + std::to_string(u);
+      if (!block(p + ".r0", 2 * high, low, len, e.up[u][0]) ||
+          !block(p + ".r1", low, low, len, e.up[u][1]) ||
+          !conv(p + ".us", low, low, 4, fe::hip::kConvTranspose, e.us[u], true))
+        return false;
+      e.us[u].op.lin = static_cast<int>(len);
+      e.us[u].op.lout = static_cast<int>(2 * len);
+      len *= 2;
+    }
+    if (!conv("dp.f.c", c.dims[0], c.dims[0], c.kernel, fe::hip::kConvSame, e.fconv) ||
+        !norm("dp.f.n", c.dims[0], e.fnorm) ||
+        !conv("dp.f.o", c.action_dim, c.dims[0], 1, fe::hip::kConvSame, e.fout))
+      return false;
+    e.fconv.op.lin = e.fconv.op.lout = static_cast<int>(c.horizon);
+    e.fout.op.lin = e.fout.op.lout = static_cast<int>(c.horizon);
+
+    // FiLM tables: W_t^T [tdim][F], W_c^T [cond][F], bias [F].
+    const std::size_t F = e.film_total;
+    e.film_wt = plan.take(c.tdim * F * 4);
+    e.film_wc = plan.take(c.cond_dim * F * 4);
+    e.film_bias = plan.take(F * 4);
+
+    // Per-call buffers.  U-Net evaluations per call: diffusion <= T steps, flow RK4 4 per step.
+    e.max_nfe = std::max<std::size_t>(c.train_timesteps, 1024);
+    e.time_m = plan.take(e.max_nfe * c.tdim * 4);
+    e.film_table = plan.take(e.max_nfe * F * 4);
+    e.film_cond = plan.take(B * F * 4);
+    const std::size_t v = c.horizon * c.action_dim;
+    e.x_state = plan.take(B * v * 4);
+    e.x_in = plan.take(B * v * 4);
+    e.k_stages = plan.take(4 * B * v * 4);
+    e.in_cond = plan.take(B * c.cond_dim * 4);
+    e.in_noise = plan.take(B * v * 4);
+    e.out_action = plan.take(B * v * 4);
+    e.seed_dev = plan.take(8);
+
+    // Activations.
+    for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+      const Block& r0 = e.up[u][0];
+      e.concat[u] = plan.take(B * r0.ic * r0.len * 4);
+    }
+    auto acts = [&](Block& blk) {
+      blk.h1_off = plan.take(B * blk.oc * blk.len * 4);
+      blk.h2_off = plan.take(B * blk.oc * blk.len * 4);
+      if (!blk.identity) blk.r_off = plan.take(B * blk.oc * blk.len * 4);
+    };
+    for (std::size_t s = 0; s < c.stages; ++s) {
+      for (int k = 0; k < 2; ++k) acts(e.down[s][k]);
+      Block& r0 = e.down[s][0];
+      r0.out_off = plan.take(B * r0.oc * r0.len * 4);
+      r0.out_stride = r0.oc * r0.len;
+      Block& r1 = e.down[s][1];
+      if (s >= 1) {
+        // Skip tensor: second half of the concat buffer of up stage S-1-s.
+        const std::size_t u = c.stages - 1 - s;
+        r1.out_off = e.concat[u] + r1.oc * r1.len * 4;
+        r1.out_stride = 2 * r1.oc * r1.len;
+      } else {
+        r1.out_off = plan.take(B * r1.oc * r1.len * 4);
+        r1.out_stride = r1.oc * r1.len;
+      }
+      if (s + 1 < c.stages) e.ds_out[s] = plan.take(B * r1.oc * (r1.len / 2) * 4);
+    }
+    for (int m = 0; m < 2; ++m) acts(e.mid[m]);
+    e.mid[0].out_off = plan.take(B * bottom * e.mid[0].len * 4);
+    e.mid[0].out_stride = bottom * e.mid[0].len;
+    e.mid[1].out_off = e.concat[0];
+    e.mid[1].out_stride = 2 * bottom * e.mid[1].len;
+    for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+      for (int k = 0; k < 2; ++k) {
+        Block& blk = e.up[u][k];
+        acts(blk);
+        blk.out_off = plan.take(B * blk.oc * blk.len * 4);
+        blk.out_stride = blk.oc * blk.len;
+      }
+    }
+    e.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
+    e.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
+    return true;
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+// Uploads with repacking.
+// ---------------------------------------------------------------------------------------------
+hipError_t upload(void* dst, const void* src, std::size_t bytes) {
+  return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+}
+
+void widen(const fe::TensorInfo* t, std::vector<float>& out) {
+  const std::size_t n = t->elements();
+  out.resize(n);
+  if (!t->bf16) {
+    std::memcpy(out.data(), t->data, n * 4);
+  } else {
+    const auto* bits = static_cast<const std::uint16_t*>(t->data);
+    for (std::size_t i = 0; i < n; ++i) {
+      const std::uint32_t w = static_cast<std::uint32_t>(bits[i]) << 16;
+      std::memcpy(&out[i], &w, 4);
+    }
+  }
+}
+
+// Conv [OC][IC][K] (or ConvTranspose [IC][OC][K]) -> [OC][K][IC], keeping the storage dtype.
+hipError_t upload_conv(FeEngine& e, const ConvSlot& s) {
+  const auto* w = s.w_src;
+  const std::size_t oc = s.op.oc, ic = s.op.ic, k = s.op.k;
+  const std::size_t esz = w->bf16 ? 2 : 4;
+  std::vector<char> packed(oc * ic * k * esz);
+  const char* src = static_cast<const char*>(w->data);
+  for (std::size_t o = 0; o < oc; ++o)
+    for (std::size_t kk = 0; kk < k; ++kk)
+      for (std::size_t i = 0; i < ic; ++i) {
+        const std::size_t from = s.transpose_storage ? (i * oc + o) * k + kk : (o * ic + i) * k + kk;
+        std::memcpy(&packed[((o * k + kk) * ic + i) * esz], src + from * esz, esz);
+      }
+  hipError_t st = upload(e.ptr<char>(s.w_off), packed.data(), packed.size());
+  if (st != hipSuccess) return st;
+  return upload(e.ptr<char>(s.b_off), s.b_src->data, oc * 4);
+}
+
+hipError_t upload_norm(FeEngine& e, const NormSlot& n) {
+  hipError_t st = upload(e.ptr<char>(n.g_off), n.g_src->data, n.g_src->bytes);
+  if (st != hipSuccess) return st;
+  return upload(e.ptr<char>(n.b_off), n.b_src->data, n.b_src->bytes);
+}
+
+hipError_t upload_block(FeEngine& e, const Block& b, std::vector<float>& wt, std::vector<float>& wc,
+                        std::vector<float>& bias) {
+  hipError_t st;
+  if ((st = upload_conv(e, b.c1)) != hipSuccess || (st = upload_conv(e, b.c2)) != hipSuccess ||
+      (st = upload_norm(e, b.n1)) != hipSuccess || (st = upload_norm(e, b.n2)) != hipSuccess)
+    return st;
+  if (!b.identity && (st = upload_conv(e, b.res)) != hipSuccess) return st;
+  // FiLM linear [2 oc][tdim + cond] split into the transposed time and condition tables.
+  std::vector<float> w;
+  widen(b.film_w, w);
+  const std::size_t F = e.film_total, td = e.cfg.tdim, cd = e.cfg.cond_dim;
+  const float* bb = static_cast<const float*>(b.film_b->data);
+  for (std::size_t r = 0; r < 2 * b.oc; ++r) {
+    const std::size_t f = b.film_off + r;
+    for (std::size_t k = 0; k < td; ++k) wt[k * F + f] = w[r * (td + cd) + k];
+    for (std::size_t k = 0; k < cd; ++k) wc[k * F + f] = w[r * (td + cd) + td + k];
+    bias[f] = bb[r];
+  }
+  return hipSuccess;
+}
+
+hipError_t upload_weights(FeEngine& e, const fe::Checkpoint& ck) {
+  const Config& c = e.cfg;
+  hipError_t st;
+  std::vector<float> tmp;
+  auto linear = [&](const char* name, std::size_t woff, std::size_t boff) -> hipError_t {
+    const std::string p(name);
+    widen(ck.find(p + ".w"), tmp);
+    hipError_t s = upload(e.ptr<char>(woff), tmp.data(), tmp.size() * 4);
+    if (s != hipSuccess) return s;
+    const fe::TensorInfo* b = ck.find(p + ".b");
+    return upload(e.ptr<char>(boff), b->data, b->bytes);
+  };
+  if ((st = linear("dp.te1", e.te1w, e.te1b)) != hipSuccess) return st;
+  if ((st = linear("dp.te2", e.te2w, e.te2b)) != hipSuccess) return st;
+  if ((st = upload(e.ptr<char>(e.amin), ck.find("dp.action_min")->data, c.action_dim * 4)) !=
+          hipSuccess ||
+      (st = upload(e.ptr<char>(e.amax), ck.find("dp.action_max")->data, c.action_dim * 4)) !=
+          hipSuccess)
+    return st;
+  const std::size_t F = e.film_total;
+  std::vector<float> wt(c.tdim * F), wc(c.cond_dim * F), bias(F);
+  for (std::size_t s = 0; s < c.stages; ++s) {
+    for (int k = 0; k < 2; ++k)
+      if ((st = upload_block(e, e.down[s][k], wt, wc, bias)) != hipSuccess) return st;
+    if (s + 1 < c.stages && (st = upload_conv(e, e.ds[s])) != hipSuccess) return st;
+  }
+  for (int m = 0; m < 2; ++m)
+    if ((st = upload_block(e, e.mid[m], wt, wc, bias)) != hipSuccess) return st;
+  for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+    for (int k = 0; k < 2; ++k)
+      if ((st = upload_block(e, e.up[u][k], wt, wc, bias)) != hipSuccess) return st;
+    if ((st = upload_conv(e, e.us[u])) != hipSuccess) return st;
+  }
+  if ((st = upload_conv(e, e.fconv)) != hipSuccess || (st = upload_norm(e, e.fnorm)) != hipSuccess ||
+      (st = upload_conv(e, e.fout)) != hipSuccess)
+    return st;
+  if ((st = upload(e.ptr<char>(e.film_wt), wt.data(), wt.size() * 4)) != hipSuccess ||
+      (st = upload(e.ptr<char>(e.film_wc), wc.data(), wc.size() * 4)) != hipSuccess ||
+      (st = upload(e.ptr<char>(e.film_bias), bias.data(), bias.size() * 4)) != hipSuccess)
+    return st;
+  return hipSuccess;
+}
+
+// Fills device pointers of the conv ops once the arena base is known.
+void bind(FeEngine& e, ConvSlot& s) {
+  s.op.w = e.arena + s.w_off;
+  s.op.b = e.ptr(s.b_off);
+}
+
+void bind_all(FeEngine& e) {
+  const Config& c = e.cfg;
+  auto blk = [&](Block& b) {
+    bind(e, b.c1);
+    bind(e, b.c2);
+    if (!b.identity) bind(e, b.res);
+  };
+  for (std::size_t s = 0; s < c.stages; ++s) {
+    blk(e.down[s][0]);
+    blk(e.down[s][1]);
+    if (s + 1 < c.stages) bind(e, e.ds[s]);
+  }
+  blk(e.mid[0]);
+  blk(e.mid[1]);
+  for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+    blk(e.up[u][0]);
+    blk(e.up[u][1]);
+    bind(e, e.us[u]);
+  }
+  bind(e, e.fconv);
+  bind(e, e.fout);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Enqueue helpers.
+// ---------------------------------------------------------------------------------------------
+#define FE_TRY(expr)                         \
+  do {                                       \
+    const hipError_t fe_st_ = (expr);        \
+    if (fe_st_ != hipSuccess) return fe_st_; \
+  } while (0)
+
+hipError_t enqueue_block(FeEngine& e, const Block& b, const float* x, std::int64_t xs, int batch,
+                         const float* film_row) {
+  using namespace fe::hip;
+  hipStream_t s = e.stream;
+  const std::int64_t act = static_cast<std::int64_t>(b.oc * b.len);
+  float* h1 = e.ptr(b.h1_off);
+  float* h2 = e.ptr(b.h2_off);
+  FE_TRY(conv(b.c1.op, x, xs, View{h1, act}, batch, s));
+  const float* res = x;
+  std::int64_t res_stride = xs;
+  if (!b.identity) {
+    float* r = e.ptr(b.r_off);
+    FE_TRY(conv(b.res.op, x, xs, View{r, act}, batch, s));
+    res = r;
+    res_stride = act;
+  }
+  NormActOp n1{};
+  n1.gamma = e.ptr(b.n1.g_off);
+  n1.beta = e.ptr(b.n1.b_off);
+  n1.c = static_cast<int>(b.oc);
+  n1.len = static_cast<int>(b.len);
+  n1.groups = static_cast<int>(e.cfg.groups);
+  n1.film_time = film_row;
+  n1.film_cond = e.ptr(e.film_cond);
+  n1.film_cond_stride = static_cast<std::int64_t>(e.film_total);
+  n1.film_off = static_cast<int>(b.film_off);
+  FE_TRY(norm_act(n1, h1, act, View{h1, act}, batch, s));
+  FE_TRY(conv(b.c2.op, h1, act, View{h2, act}, batch, s));
+  NormActOp n2{};
+  n2.gamma = e.ptr(b.n2.g_off);
+  n2.beta = e.ptr(b.n2.b_off);
+  n2.c = static_cast<int>(b.oc);
+  n2.len = static_cast<int>(b.len);
+  n2.groups = static_cast<int>(e.cfg.groups);
+  n2.res = res;
+  n2.res_stride = res_stride;
+  return norm_act(n2, h2, act, View{e.ptr(b.out_off), static_cast<std::int64_t>(b.out_stride)},
+                  batch, s);
+}
+
+// One U-Net evaluation on xin (FiLM time row `film_row`), ending with `upd`.
+hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::UpdateOp upd) {
+  using namespace fe::hip;
+  const Config& c = e.cfg;
+  hipStream_t s = e.stream;
+  const float* x = e.ptr(e.x_in);
+  std::int64_t xs = static_cast<std::int64_t>(c.action_dim * c.horizon);
+  for (std::size_t st = 0; st < c.stages; ++st) {
+    for (int k = 0; k < 2; ++k) {
+      const Block& b = e.down[st][k];
+      FE_TRY(enqueue_block(e, b, x, xs, batch, film_row));
+      x = e.ptr(b.out_off);
+      xs = static_cast<std::int64_t>(b.out_stride);
+    }
+    if (st + 1 < c.stages) {
+      const ConvSlot& d = e.ds[st];
+      float* y = e.ptr(e.ds_out[st]);
+      const std::int64_t ys = static_cast<std::int64_t>(d.op.oc) * d.op.lout;
+      FE_TRY(conv(d.op, x, xs, View{y, ys}, batch, s));
+      x = y;
+      xs = ys;
+    }
+  }
+  for (int m = 0; m < 2; ++m) {
+    const Block& b = e.mid[m];
+    FE_TRY(enqueue_block(e, b, x, xs, batch, film_row));
+    x = e.ptr(b.out_off);
+    xs = static_cast<std::int64_t>(b.out_stride);
+  }
+  for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+    // Input of up stage u is its concat buffer [x ; skip].
+    x = e.ptr(e.concat[u]);
+    xs = static_cast<std::int64_t>(e.up[u][0].ic * e.up[u][0].len);
+    for (int k = 0; k < 2; ++k) {
+      const Block& b = e.up[u][k];
+      FE_TRY(enqueue_block(e, b, x, xs, batch, film_row));
+      x = e.ptr(b.out_off);
+      xs = static_cast<std::int64_t>(b.out_stride);
+    }
+    const ConvSlot& up = e.us[u];
+    View y;
+    if (u + 2 < c.stages) {
+      y.p = e.ptr(e.concat[u + 1]);
+      y.stride = static_cast<std::int64_t>(e.up[u + 1][0].ic * e.up[u + 1][0].len);
+    } else {
+      y.p = e.ptr(e.final_in);
+      y.stride = static_cast<std::int64_t>(c.dims[0] * c.horizon);
+    }
+    FE_TRY(conv(up.op, x, xs, y, batch, s));
+  }
+  const std::int64_t fs = static_cast<std::int64_t>(c.dims[0] * c.horizon);
+  float* fo = e.ptr(e.fconv_out);
+  FE_TRY(conv(e.fconv.op, e.ptr(e.final_in), fs, View{fo, fs}, batch, s));
+  NormActOp fn{};
+  fn.gamma = e.ptr(e.fnorm.g_off);
+  fn.beta = e.ptr(e.fnorm.b_off);
+  fn.c = static_cast<int>(c.dims[0]);
+  fn.len = static_cast<int>(c.horizon);
+  fn.groups = static_cast<int>(kFinalNormGroups);
+  FE_TRY(norm_act(fn, fo, fs, View{fo, fs}, batch, s));
+  upd.c0 = static_cast<int>(c.dims[0]);
+  upd.horizon = static_cast<int>(c.horizon);
+  upd.action_dim = static_cast<int>(c.action_dim);
+  upd.h = fo;
+  upd.wo = static_cast<const float*>(e.fout.op.w);
+  upd.bo = e.fout.op.b;
+  return update(upd, batch, s);
+}
+
+// FiLM tables for `count` U-Net evaluations and the per-sample condition part.
+hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int batch) {
+  using namespace fe::hip;
+  const Config& c = e.cfg;
+  const int F = static_cast<int>(e.film_total);
+  FE_TRY(time_mlp(ts, count, e.ptr(e.te1w), e.ptr(e.te1b), e.ptr(e.te2w), e.ptr(e.te2b),
+                  static_cast<int>(c.tdim), e.ptr(e.time_m), e.stream));
+  // The time MLP output already carries its Mish (the reference applies Mish to the whole FiLM
+  // input [t_emb ; cond] once, diffusion.cc:818-820).
+  FE_TRY(film_gemm(e.ptr(e.time_m), static_cast<std::int64_t>(c.tdim), count,
+                   static_cast<int>(c.tdim), e.ptr(e.film_wt), e.ptr(e.film_bias), F, false,
+                   e.ptr(e.film_table), F, e.stream));
+  return film_gemm(e.ptr(e.in_cond), static_cast<std::int64_t>(c.cond_dim), batch,
+                   static_cast<int>(c.cond_dim), e.ptr(e.film_wc), nullptr, F, true,
+                   e.ptr(e.film_cond), F, e.stream);
+}
+
+// Whole DDIM/DDPM sampling call (diffusion.cc:916-1035) for `batch` samples.
+hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int scheduler,
+                             const float* alphas) {
+  using namespace fe::hip;
+  const Config& c = e.cfg;
+  const std::size_t ratio = c.train_timesteps / steps;
+  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_state), batch,
+                      static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
+  TimeSpec ts;
+  ts.mode = kTimesDiffusion;
+  ts.steps = static_cast<int>(steps);
+  ts.ratio = static_cast<int>(ratio);
+  FE_TRY(enqueue_film(e, ts, static_cast<int>(steps), batch));
+  std::uint64_t noisy_steps = 0;
+  for (std::size_t i = 0; i < steps; ++i) {
+    const std::size_t t = (steps - 1 - i) * ratio;
+    const std::ptrdiff_t prev = static_cast<std::ptrdiff_t>(t) - static_cast<std::ptrdiff_t>(ratio);
+    const float at = alphas[t];
+    const float ap = prev >= 0 ? alphas[prev] : 1.0f;
+    const float bt = 1.0f - at;
+    UpdateOp u{};
+    u.x = e.ptr(e.x_state);
+    u.xin = e.ptr(e.x_state);
+    u.sqrt_at = std::sqrt(at);
+    u.sqrt_bt = std::sqrt(bt);
+    u.clip = c.clip ? 1 : 0;
+    u.clip_range = c.clip_range;
+    if (scheduler == FE_DIFFUSION_DDIM) {
+      u.kind = kUpdateDDIM;
+      u.sqrt_ap = std::sqrt(ap);
+      u.sqrt_1map = std::sqrt(1.0f - ap);
+    } else {
+      // diffusion.cc:1006-1023.
+      const float ca = at / ap, cb = 1.0f - ca;
+      u.kind = kUpdateDDPM;
+      u.coef_x0 = std::sqrt(ap) * cb / std::max(bt, 1e-20f);
+      u.coef_x = std::sqrt(ca) * (1.0f - ap) / std::max(bt, 1e-20f);
+      const float var = ((1.0f - ap) / std::max(bt, 1e-20f)) * cb;
+      u.sigma = std::sqrt(std::max(var, 1e-20f));
+      u.seed = e.ptr<std::uint64_t>(e.seed_dev);
+      u.add_noise = prev >= 0 ? 1 : 0;
+      u.noise_offset = noisy_steps * e.values;
+      if (prev >= 0) ++noisy_steps;
+    }
+    const float* row = e.ptr(e.film_table) + i * e.film_total;
+    // DDIM and DDPM read xin == x: the state is the U-Net input.
+    FE_TRY(enqueue_unet(e, batch, row, u));
+  }
+  return finish_sample(e.ptr(e.x_state), e.ptr(e.amin), e.ptr(e.amax), e.ptr(e.out_action), batch,
+                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream);
+}
+
+// Flow-ODE sampling (flow.cc:291-318) with the U-Net as velocity field.
+hipError_t enqueue_flow(FeEngine& e, int batch, std::size_t steps, int method) {
+  using namespace fe::hip;
+  const Config& c = e.cfg;
+  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
+                      static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
+  const int stages = method == FE_SOLVER_RK4 ? 4 : (method == FE_SOLVER_HEUN ? 2 : 1);
+  TimeSpec ts;
+  ts.mode = kTimesFlow;
+  ts.steps = static_cast<int>(steps);
+  ts.method = method;
+  const int nfe = static_cast<int>(steps) * stages;
+  FE_TRY(enqueue_film(e, ts, nfe, batch));
+  const float dt = 1.0f / static_cast<float>(steps);
+  const float half_dt = 0.5f * dt;
+  for (int n = 0; n < nfe; ++n) {
+    const int j = n % stages;
+    UpdateOp u{};
+    u.x = e.ptr(e.x_state);
+    u.xin = e.ptr(e.x_in);
+    u.kbuf = e.ptr(e.k_stages);
+    u.dt = dt;
+    if (stages == 1) {
+      u.kind = kUpdateEuler;
+    } else if (stages == 2) {
+      if (j == 0) {
+        u.kind = kUpdateStage;
+        u.slot = 0;
+        u.dt = dt;
+      } else {
+        u.kind = kUpdateHeun;
+      }
+    } else {
+      if (j < 3) {
+        u.kind = kUpdateStage;
+        u.slot = j;
+        u.dt = j < 2 ? half_dt : dt;
+      } else {
+        u.kind = kUpdateRK4;
+      }
+    }
+    FE_TRY(enqueue_unet(e, batch, e.ptr(e.film_table) + static_cast<std::size_t>(n) * e.film_total,
+                        u));
+  }
+  return finish_sample(e.ptr(e.x_state), nullptr, nullptr, e.ptr(e.out_action), batch,
+                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream);
+}
+
+std::vector<float> alphas_cumprod(std::size_t T) {
+  // diffusion.cc:186-191, 529-541: beta in double, cumulative product in float.
+  auto abar = [](double t) {
+    const double c = std::cos(((t + 0.008) / 1.008) * (3.14159265358979323846 / 2.0));
+    return c * c;
+  };
+  std::vector<float> a(T);
+  float cum = 1.0f;
+  for (std::size_t s = 0; s < T; ++s) {
+    const double b0 = static_cast<double>(s) / static_cast<double>(T);
+    const double b1 = static_cast<double>(s + 1) / static_cast<double>(T);
+    const float beta = static_cast<float>(std::min(1.0 - abar(b1) / abar(b0), 0.999));
+    cum *= 1.0f - beta;
+    a[s] = cum;
+  }
+  return a;
+}
+
+// Returns the cached graph for this shape, capturing it on first use.
+hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps, int mode,
+                     hipGraphExec_t& exec) {
+  for (auto it = e.graphs.begin(); it != e.graphs.end(); ++it)
+    if (it->kind == kind && it->batch == batch && it->steps == steps && it->mode == mode) {
+      e.graphs.splice(e.graphs.begin(), e.graphs, it);
+      exec = it->exec;
+      return hipSuccess;
+    }
+  FE_TRY(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal));
+  hipError_t st;
+  if (kind == 0) {
+    const std::vector<float> alphas = alphas_cumprod(e.cfg.train_timesteps);
+    st = enqueue_diffusion(e, static_cast<int>(batch), steps, mode, alphas.data());
+  } else {
+    st = enqueue_flow(e, static_cast<int>(batch), steps, mode);
+  }
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(e.stream, &graph);
+  if (st != hipSuccess || end != hipSuccess) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return st != hipSuccess ? st : end;
+  }
+  hipGraphExec_t inst = nullptr;
+  st = hipGraphInstantiate(&inst, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (st != hipSuccess) return st;
+  if (e.graphs.size() >= kGraphCache) {
+    (void)hipGraphExecDestroy(e.graphs.back().exec);
+    e.graphs.pop_back();
+  }
+  e.graphs.push_front(GraphEntry{kind, mode, batch, steps, inst});
+  exec = inst;
+  return hipSuccess;
+}
+
+int hip_fail(const char* what, hipError_t st) {
+  set_error(std::string(what) + ": " + hipGetErrorString(st));
+  return FE_STATUS_RESOURCE_EXHAUSTED;
+}
+
+// Validates a sampling request (engine_runtime.cc:446-470 + extensions).
+int check_sample(const FeEngine* e, int kind, std::size_t batch, std::size_t steps, int mode) {
+  if (kind == 0) {
+    if (e->cfg.prediction != 0) {
+      set_error("Model has no Diffusion Policy head to sample from");
+      return FE_STATUS_UNSUPPORTED_MODEL;
+    }
+    if (mode != FE_DIFFUSION_DDIM && mode != FE_DIFFUSION_DDPM) {
+      set_error("Diffusion scheduler must be FE_DIFFUSION_DDIM or FE_DIFFUSION_DDPM");
+      return FE_STATUS_INVALID_SOLVER;
+    }
+    if (steps == 0 || steps > e->cfg.train_timesteps) {
+      set_error("Diffusion inference steps must be between 1 and the training timestep count");
+      return FE_STATUS_INVALID_ARGUMENT;
+    }
+  } else {
+    if (e->cfg.prediction != 1) {
+      set_error("Model has no flow head to sample from");
+      return FE_STATUS_UNSUPPORTED_MODEL;
+    }
+    if (mode < FE_SOLVER_EULER || mode > FE_SOLVER_RK4) {
+      set_error("Invalid solver method");
+      return FE_STATUS_INVALID_SOLVER;
+    }
+    const std::size_t stages = mode == FE_SOLVER_RK4 ? 4 : (mode == FE_SOLVER_HEUN ? 2 : 1);
+    if (steps == 0 || steps * stages > e->max_nfe) {
+      set_error("Flow solver steps out of range");
+      return FE_STATUS_INVALID_ARGUMENT;
+    }
+  }
+  if (batch == 0 || batch > e->max_batch) {
+    set_error("Batch size must be between 1 and the engine's max batch");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  return FE_STATUS_OK;
+}
+
+// Replays the sampling graph; inputs already in the engine's device input buffers.
+int run_graph(FeEngine* e, int kind, std::size_t batch, std::size_t steps, int mode) {
+  hipGraphExec_t exec = nullptr;
+  hipError_t st = get_graph(*e, kind, batch, steps, mode, exec);
+  if (st != hipSuccess) return hip_fail("Failed to build sampling graph", st);
+  if ((st = hipEventRecord(e->ev0, e->stream)) != hipSuccess ||
+      (st = hipGraphLaunch(exec, e->stream)) != hipSuccess ||
+      (st = hipEventRecord(e->ev1, e->stream)) != hipSuccess)
+    return hip_fail("Sampling graph launch failed", st);
+  e->timed = true;
+  return FE_STATUS_OK;
+}
+
+int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, std::size_t batch,
+                std::size_t steps, int mode, std::uint64_t seed, float* action) {
+  const int rc = check_sample(e, kind, batch, steps, mode);
+  if (rc != FE_STATUS_OK) return rc;
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  const Config& c = e->cfg;
+  const std::size_t nc = batch * c.cond_dim, nv = batch * e->values;
+  std::memcpy(e->pin_cond, cond, nc * 4);
+  std::memcpy(e->pin_noise, noise, nv * 4);
+  *e->pin_seed = seed;
+  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), e->pin_cond, nc * 4, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->in_noise), e->pin_noise, nv * 4, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->seed_dev), e->pin_seed, 8, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess)
+    return hip_fail("Input upload failed", st);
+  const int r = run_graph(e, kind, batch, steps, mode);
+  if (r != FE_STATUS_OK) return r;
+  if ((st = hipMemcpyAsync(e->pin_action, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToHost,
+                           e->stream)) != hipSuccess ||
+      (st = hipStreamSynchronize(e->stream)) != hipSuccess)
+    return hip_fail("Sampling failed", st);
+  std::memcpy(action, e->pin_action, nv * 4);
+  return FE_STATUS_OK;
+}
+
+std::size_t env_max_batch() {
+  const char* v = std::getenv("FLOWEDGE_MAX_BATCH");
+  if (v == nullptr || *v == '\0') return 256;
+  char* end = nullptr;
+  const unsigned long n = std::strtoul(v, &end, 10);
+  return (end && *end == '\0' && n > 0 && n <= 65535) ? n : 0;
+}
+
+fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned threads) {
+  if (threads > kMaxPoolThreads) {
+    set_error("Worker thread count must be from 0 through 8");
+    return nullptr;
+  }
+  if (!ck) {
+    set_error("Invalid null model weights");
+    return nullptr;
+  }
+  if (env_flag("FLOWEDGE_CUDA_FORCE_HOST")) {
+    set_error("FLOWEDGE_CUDA_FORCE_HOST=1 but this library has no host kernels: the U-Net runs "
+              "only on the GPU");
+    return nullptr;
+  }
+  std::unique_ptr<FeEngine> e;
+  try {
+    e.reset(new FeEngine());
+  } catch (const std::bad_alloc&) {
+    set_error("Out of host memory");
+    return nullptr;
+  }
+  e->threads = threads;
+  std::string err;
+  if (!parse_config(*ck, e->cfg, err) || !supported_shape(e->cfg, err)) {
+    set_error(err);
+    return nullptr;
+  }
+  e->max_batch = env_max_batch();
+  if (e->max_batch == 0) {
+    set_error("FLOWEDGE_MAX_BATCH must be an integer from 1 through 65535");
+    return nullptr;
+  }
+  e->values = e->cfg.horizon * e->cfg.action_dim;
+  Builder builder{*e, *ck, Plan{}, {}};
+  if (!builder.build()) {
+    set_error(builder.err);
+    return nullptr;
+  }
+  e->arena_bytes = builder.plan.size;
+
+  int count = 0;
+  hipError_t st = hipGetDeviceCount(&count);
+  if (st != hipSuccess || count == 0) {
+    set_error("No HIP device available (the Diffusion Policy engine runs on the GPU only)");
+    return nullptr;
+  }
+  if ((st = hipGetDevice(&e->device)) != hipSuccess) {
+    hip_fail("hipGetDevice", st);
+    return nullptr;
+  }
+  if (env_flag("FLOWEDGE_HIP_FAIL_ALLOC")) {
+    set_error("Device arena allocation failed (FLOWEDGE_HIP_FAIL_ALLOC=1)");
+    return nullptr;
+  }
+  st = hipMalloc(reinterpret_cast<void**>(&e->arena), e->arena_bytes);
+  if (st != hipSuccess) {
+    e->arena = nullptr;
+    hip_fail("Device arena allocation failed", st);
+    return nullptr;
+  }
+  g_device_allocs.fetch_add(1);
+  const std::size_t B = e->max_batch, nv = B * e->values, nc = B * e->cfg.cond_dim;
+  const std::size_t pin_bytes = (nc + 2 * nv) * 4 + 64;
+  void* pin = nullptr;
+  if ((st = hipHostMalloc(&pin, pin_bytes, hipHostMallocDefault)) != hipSuccess) {
+    hip_fail("Pinned staging allocation failed", st);
+    return nullptr;
+  }
+  e->pin_cond = static_cast<float*>(pin);
+  e->pin_noise = e->pin_cond + nc;
+  e->pin_action = e->pin_noise + nv;
+  e->pin_seed = reinterpret_cast<std::uint64_t*>(
+      (reinterpret_cast<std::uintptr_t>(e->pin_action + nv) + 15) & ~std::uintptr_t{15});
+  if ((st = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
+      (st = hipEventCreate(&e->ev0)) != hipSuccess || (st = hipEventCreate(&e->ev1)) != hipSuccess) {
+    hip_fail("Stream creation failed", st);
+    return nullptr;
+  }
+  bind_all(*e);
+  if ((st = upload_weights(*e, *ck)) != hipSuccess) {
+    hip_fail("Weight upload failed", st);
+    return nullptr;
+  }
+  return e.release();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// C ABI.
+// ---------------------------------------------------------------------------------------------
+extern "C" {
+
+const char* fe_engine_last_error(void) { return t_error; }
+
+fe_weights* fe_weights_load(const char* path) {
+  clear_error();
+  if (path == nullptr) {
+    set_error("Invalid null model path");
+    return nullptr;
+  }
+  std::string err;
+  auto ck = fe::Checkpoint::open(path, err);
+  if (!ck) {
+    set_error(err);
+    return nullptr;
+  }
+  return new (std::nothrow) FeWeights{std::move(ck)};
+}
+
+size_t fe_weights_size_bytes(const fe_weights* weights) {
+  return weights != nullptr && weights->ck ? weights->ck->weight_bytes() : 0;
+}
+
+void fe_weights_free(fe_weights* weights) { delete weights; }
+
+static bool env_threads(unsigned& out) {
+  const char* v = std::getenv("FLOWEDGE_THREADS");
+  if (v == nullptr || *v == '\0') {
+    out = 0;
+    return true;
+  }
+  char* end = nullptr;
+  const unsigned long n = std::strtoul(v, &end, 10);
+  if (!end || *end != '\0' || n > kMaxPoolThreads) {
+    set_error("FLOWEDGE_THREADS must be an integer from 0 through 8");
+    return false;
+  }
+  out = static_cast<unsigned>(n);
+  return true;
+}
+
+fe_engine* fe_engine_create_from_weights(const fe_weights* weights, unsigned worker_threads) {
+  clear_error();
+  if (weights == nullptr) {
+    set_error("Invalid null model weights");
+    return nullptr;
+  }
+  return create_engine(weights->ck, worker_threads);
+}
+
+fe_engine* fe_engine_create_from_weights_auto(const fe_weights* weights) {
+  clear_error();
+  if (weights == nullptr) {
+    set_error("Invalid null model weights");
+    return nullptr;
+  }
+  unsigned threads = 0;
+  return env_threads(threads) ? create_engine(weights->ck, threads) : nullptr;
+}
+
+fe_engine* fe_engine_load_with_threads(const char* path, unsigned worker_threads) {
+  clear_error();
+  if (path == nullptr) {
+    set_error("Invalid null model path");
+    return nullptr;
+  }
+  std::string err;
+  auto ck = fe::Checkpoint::open(path, err);
+  if (!ck) {
+    set_error(err);
+    return nullptr;
+  }
+  return create_engine(std::move(ck), worker_threads);
+}
+
+fe_engine* fe_engine_load(const char* path) {
+  clear_error();
+  unsigned threads = 0;
+  if (!env_threads(threads)) return nullptr;
+  if (path == nullptr) {
+    set_error("Invalid null model path");
+    return nullptr;
+  }
+  std::string err;
+  auto ck = fe::Checkpoint::open(path, err);
+  if (!ck) {
+    set_error(err);
+    return nullptr;
+  }
+  return create_engine(std::move(ck), threads);
+}
+
+void fe_engine_free(fe_engine* engine) {
+  if (engine) (void)hipSetDevice(engine->device);
+  delete engine;
+}
+
+unsigned fe_engine_thread_count(const fe_engine* engine) {
+  return engine != nullptr ? engine->threads : 0u;
+}
+
+int fe_engine_cuda_resident(const fe_engine* engine) { return engine != nullptr ? 1 : 0; }
+
+int fe_engine_model_metadata(const fe_engine* engine, fe_model_metadata* metadata) {
+  clear_error();
+  if (engine == nullptr || metadata == nullptr) {
+    set_error("Invalid arguments to fe_engine_model_metadata");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  fe_model_metadata m{};
+  m.struct_size = sizeof(m);
+  m.protocol_version = FE_PROTOCOL_VERSION;
+  m.architecture = FE_ARCH_DIFFUSION_HEAD;
+  m.precision = engine->any_bf16 ? FE_PRECISION_MIXED : FE_PRECISION_F32;
+  m.action_dim = engine->cfg.action_dim;
+  m.condition_dim = engine->cfg.cond_dim;
+  *metadata = m;
+  return FE_STATUS_OK;
+}
+
+size_t fe_engine_action_dim(const fe_engine* engine) {
+  return engine != nullptr ? engine->cfg.action_dim : 0;
+}
+
+size_t fe_engine_action_horizon(const fe_engine* engine) {
+  return engine != nullptr ? engine->cfg.horizon : 0;
+}
+
+size_t fe_engine_condition_dim(const fe_engine* engine) {
+  return engine != nullptr ? engine->cfg.cond_dim : 0;
+}
+
+int fe_engine_diffusion_metadata(const fe_engine* engine, fe_diffusion_metadata* metadata) {
+  clear_error();
+  if (engine == nullptr || metadata == nullptr) {
+    set_error("Invalid arguments to fe_engine_diffusion_metadata");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  fe_diffusion_metadata m{};
+  m.struct_size = sizeof(m);
+  m.protocol_version = FE_PROTOCOL_VERSION;
+  m.clip_sample = engine->cfg.clip ? 1u : 0u;
+  m.action_dim = engine->cfg.action_dim;
+  m.condition_dim = engine->cfg.cond_dim;
+  m.horizon = engine->cfg.horizon;
+  m.action_steps = engine->cfg.action_steps;
+  m.observation_steps = engine->cfg.obs_steps;
+  m.train_timesteps = engine->cfg.train_timesteps;
+  m.clip_sample_range = engine->cfg.clip_range;
+  *metadata = m;
+  return FE_STATUS_OK;
+}
+
+int fe_engine_sample_diffusion_batch(fe_engine* engine, const float* condition,
+                                     const float* noise, size_t batch, size_t steps,
+                                     int scheduler, uint64_t seed, float* action) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || noise == nullptr || action == nullptr ||
+      steps == 0 || batch == 0) {
+    set_error("Invalid arguments to fe_engine_sample_diffusion");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (scheduler != FE_DIFFUSION_DDIM && scheduler != FE_DIFFUSION_DDPM) {
+    set_error("Diffusion scheduler must be FE_DIFFUSION_DDIM or FE_DIFFUSION_DDPM");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  return sample_host(engine, 0, condition, noise, batch, steps, scheduler, seed, action);
+}
+
+int fe_engine_sample_diffusion(fe_engine* engine, const float* condition, const float* noise,
+                               size_t steps, int scheduler, uint64_t seed, float* action) {
+  return fe_engine_sample_diffusion_batch(engine, condition, noise, 1, steps, scheduler, seed,
+                                          action);
+}
+
+int fe_engine_sample_condition_batch(fe_engine* engine, const float* condition,
+                                     const float* noise, size_t batch, size_t steps, int method,
+                                     float* action) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || noise == nullptr || action == nullptr ||
+      steps == 0 || batch == 0) {
+    set_error("Invalid arguments to fe_engine_sample_condition");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (method < FE_SOLVER_EULER || method > FE_SOLVER_RK4) {
+    set_error("Invalid solver method");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  return sample_host(engine, 1, condition, noise, batch, steps, method, 0, action);
+}
+
+int fe_engine_sample_condition(fe_engine* engine, const float* condition, const float* noise,
+                               size_t steps, int method, float* action) {
+  return fe_engine_sample_condition_batch(engine, condition, noise, 1, steps, method, action);
+}
+
+int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
+                                      const float* normalized_sample, size_t batch,
+                                      float timestep, float* predicted_noise) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || normalized_sample == nullptr ||
+      predicted_noise == nullptr || !std::isfinite(timestep) || batch == 0) {
+    set_error("Invalid arguments to fe_engine_diffusion_denoise");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (batch > engine->max_batch) {
+    set_error("Batch size must be between 1 and the engine's max batch");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  FeEngine* e = engine;
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  const Config& c = e->cfg;
+  const std::size_t nc = batch * c.cond_dim, nv = batch * e->values;
+  std::memcpy(e->pin_cond, condition, nc * 4);
+  std::memcpy(e->pin_noise, normalized_sample, nv * 4);
+  using namespace fe::hip;
+  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), e->pin_cond, nc * 4, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->in_noise), e->pin_noise, nv * 4, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess)
+    return hip_fail("Input upload failed", st);
+  const int b = static_cast<int>(batch);
+  TimeSpec ts;
+  ts.mode = kTimesSingle;
+  ts.t0 = timestep;
+  UpdateOp u{};
+  u.kind = kUpdateDenoise;
+  u.out = e->ptr(e->out_action);
+  if ((st = begin_sample(e->ptr(e->in_noise), e->ptr(e->x_in), e->ptr(e->x_in), b,
+                         static_cast<int>(c.horizon), static_cast<int>(c.action_dim),
+                         e->stream)) != hipSuccess ||
+      (st = enqueue_film(*e, ts, 1, b)) != hipSuccess ||
+      (st = enqueue_unet(*e, b, e->ptr(e->film_table), u)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->pin_action, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToHost,
+                           e->stream)) != hipSuccess ||
+      (st = hipStreamSynchronize(e->stream)) != hipSuccess)
+    return hip_fail("Diffusion denoiser execution failed", st);
+  std::memcpy(predicted_noise, e->pin_action, nv * 4);
+  return FE_STATUS_OK;
+}
+
+int fe_engine_diffusion_denoise(fe_engine* engine, const float* condition,
+                                const float* normalized_sample, float timestep,
+                                float* predicted_noise) {
+  return fe_engine_diffusion_denoise_batch(engine, condition, normalized_sample, 1, timestep,
+                                           predicted_noise);
+}
+
+int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_dev,
+                            const float* noise_dev, size_t batch, size_t steps, int mode,
+                            uint64_t seed, float* action_dev) {
+  clear_error();
+  if (engine == nullptr || condition_dev == nullptr || noise_dev == nullptr ||
+      action_dev == nullptr || (kind != 0 && kind != 1)) {
+    set_error("Invalid arguments to fe_engine_sample_device");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  FeEngine* e = engine;
+  const int rc = check_sample(e, kind, batch, steps, mode);
+  if (rc != FE_STATUS_OK) return rc;
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  const std::size_t nc = batch * e->cfg.cond_dim, nv = batch * e->values;
+  *e->pin_seed = seed;
+  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), condition_dev, nc * 4, hipMemcpyDeviceToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->in_noise), noise_dev, nv * 4, hipMemcpyDeviceToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->seed_dev), e->pin_seed, 8, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess)
+    return hip_fail("Input copy failed", st);
+  const int r = run_graph(e, kind, batch, steps, mode);
+  if (r != FE_STATUS_OK) return r;
+  if ((st = hipMemcpyAsync(action_dev, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipStreamSynchronize(e->stream)) != hipSuccess)
+    return hip_fail("Sampling failed", st);
+  return FE_STATUS_OK;
+}
+
+int fe_engine_prepare(fe_engine* engine, int kind, size_t batch, size_t steps, int mode) {
+  clear_error();
+  if (engine == nullptr || (kind != 0 && kind != 1)) {
+    set_error("Invalid arguments to fe_engine_prepare");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const int rc = check_sample(engine, kind, batch, steps, mode);
+  if (rc != FE_STATUS_OK) return rc;
+  hipError_t st = hipSetDevice(engine->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  hipGraphExec_t exec = nullptr;
+  st = get_graph(*engine, kind, batch, steps, mode, exec);
+  return st == hipSuccess ? FE_STATUS_OK : hip_fail("Failed to build sampling graph", st);
+}
+
+size_t fe_engine_max_batch(const fe_engine* engine) {
+  return engine != nullptr ? engine->max_batch : 0;
+}
+
+size_t fe_engine_device_bytes(const fe_engine* engine) {
+  return engine != nullptr ? engine->arena_bytes : 0;
+}
+
+uint64_t fe_device_alloc_count(void) { return g_device_allocs.load(); }
+
+float fe_engine_last_device_ms(const fe_engine* engine) {
+  if (engine == nullptr || !engine->timed) return -1.0f;
+  float ms = -1.0f;
+  if (hipEventElapsedTime(&ms, engine->ev0, engine->ev1) != hipSuccess) return -1.0f;
+  return ms;
+}
+
+}  // extern "C"

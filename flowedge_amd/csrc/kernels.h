@@ -1,0 +1,129 @@
+// Device operations for the Diffusion Policy U-Net on gfx950 (internal C++ API).
+//
+// This is the layer the host runtime calls to enqueue work; it plays the role the reference's
+// `fe::cuda_ops` plays for its CUDA resident (src/core/kernels/cuda/kernels_cuda_api.h:8-120),
+// but every op here works on device-resident buffers, takes a batch dimension and is
+// enqueue-only (no allocation, no synchronisation), so a whole tick can be captured in one
+// hipGraph.
+//
+// Activation layout: [B][C][L] fp32 with channel stride L; a view may use a larger sample stride
+// (skip tensors live in the second half of an up-stage concat buffer).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fe::hip {
+
+// Convolution kinds on the path.
+enum ConvMode : int {
+  kConvSame = 0,       // stride 1, padding K/2 (K odd): residual convs, final conv, 1x1 convs
+  kConvDown = 1,       // stride 2, padding 1, K = 3: Downsample1d
+  kConvTranspose = 2,  // ConvTranspose1d stride 2, padding 1, K = 4: Upsample1d
+};
+
+struct ConvOp {
+  const void* w = nullptr;  // [OC][K][IC], fp32 or bf16 bit patterns
+  const float* b = nullptr; // [OC]
+  bool bf16 = false;
+  int mode = kConvSame;
+  int k = 1;
+  int ic = 0, oc = 0;
+  int lin = 0, lout = 0;
+};
+
+struct View {
+  float* p = nullptr;
+  std::int64_t stride = 0;  // floats between samples
+};
+
+// y = conv(x) + bias for `batch` samples.
+hipError_t conv(const ConvOp& op, const float* x, std::int64_t x_stride, View y, int batch,
+                hipStream_t stream);
+
+// GroupNorm affine, Mish, optional FiLM (scale * v + shift) and optional residual add:
+//   v = mish(gn(x));  v = scale[c] * v + shift[c];  v += res
+// FiLM values are time[off + c] + cond[b][off + c] (scale) and time[off + C + c] +
+// cond[b][off + C + c] (shift).
+struct NormActOp {
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  int c = 0, len = 0, groups = 0;
+  const float* film_time = nullptr;   // null: no FiLM
+  const float* film_cond = nullptr;
+  std::int64_t film_cond_stride = 0;
+  int film_off = 0;
+  const float* res = nullptr;         // null: no residual
+  std::int64_t res_stride = 0;
+};
+hipError_t norm_act(const NormActOp& op, const float* x, std::int64_t x_stride, View y, int batch,
+                    hipStream_t stream);
+
+// Timestep of the n-th U-Net evaluation of a sampling call, derived on the device:
+//   kTimesSingle: t = t0
+//   kTimesDiffusion: t_n = (steps - 1 - n) * ratio         (diffusion.cc:984-990)
+//   kTimesFlow: step s = n / stages, stage j = n % stages, dt = 1/steps, t = s dt, stage offsets
+//     Euler {0}, Heun {0, dt}, RK4 {0, dt/2, dt/2, dt}   (flow.cc:291-318)
+enum TimesMode : int { kTimesSingle = 0, kTimesDiffusion = 1, kTimesFlow = 2 };
+struct TimeSpec {
+  int mode = kTimesSingle;
+  float t0 = 0.0f;
+  int steps = 1;
+  int ratio = 1;
+  int method = 0;  // flow: 0 Euler, 1 Heun, 2 RK4
+};
+
+// m[n][:] = mish(te2(mish(te1(emb(t_n)) + b1)) + b2) for n < count.
+hipError_t time_mlp(const TimeSpec& times, int count, const float* w1, const float* b1,
+                    const float* w2, const float* b2, int tdim, float* m, hipStream_t stream);
+
+// out[n][f] = (bias ? bias[f] : 0) + sum_k wt[k][f] * act(in[n][k]); act = mish when `mish_in`.
+hipError_t film_gemm(const float* in, std::int64_t in_stride, int n, int kdim, const float* wt,
+                     const float* bias, int fdim, bool mish_in, float* out,
+                     std::int64_t out_stride, hipStream_t stream);
+
+// x[b][a][t] = noise[b][t][a]; also copies into `xin` when distinct.
+hipError_t begin_sample(const float* noise, float* x, float* xin, int batch, int horizon,
+                        int action_dim, hipStream_t stream);
+
+// Sampler update fused into the final 1x1 conv.  eps[b][a][t] = bo[a] + sum_c wo[a][c] h[b][c][t].
+enum UpdateKind : int {
+  kUpdateDenoise = 0,  // out[b][t][a] = eps
+  kUpdateDDIM = 1,
+  kUpdateDDPM = 2,
+  kUpdateEuler = 3,    // x += dt * v
+  kUpdateStage = 4,    // k[slot] = v; xin = x + dt * v   (Heun stage 1, RK4 stages 1-3;
+                       //   dt carries the stage coefficient dt or dt/2)
+  kUpdateHeun = 5,     // x += 0.5 dt (k0 + v)
+  kUpdateRK4 = 6,      // x += dt/6 (k0 + 2 k1 + 2 k2 + v)
+};
+struct UpdateOp {
+  int kind = kUpdateDDIM;
+  int c0 = 0, horizon = 0, action_dim = 0;
+  const float* h = nullptr;      // [B][c0][H]
+  const float* wo = nullptr;     // [A][c0]
+  const float* bo = nullptr;     // [A]
+  float* x = nullptr;            // sampler state [B][A][H]
+  float* xin = nullptr;          // U-Net input for the next NFE [B][A][H] (may equal x)
+  float* kbuf = nullptr;         // [4][B][A][H] flow stages
+  int slot = 0;
+  float* out = nullptr;          // kUpdateDenoise output [B][H][A]
+  // DDIM / DDPM scalars (host-computed as the reference does).
+  float sqrt_at = 0, sqrt_bt = 0, sqrt_ap = 0, sqrt_1map = 0;
+  float coef_x0 = 0, coef_x = 0, sigma = 0;
+  int clip = 0;
+  float clip_range = 1.0f;
+  const std::uint64_t* seed = nullptr;  // DDPM seed (device, set per call)
+  std::uint64_t noise_offset = 0;       // Gaussian stream index of this step's first value
+  int add_noise = 0;
+  float dt = 0;
+};
+hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
+
+// action[b][t][a] = (x[b][a][t] + 1) / 2 * (max - min) + min   (or a plain transpose when
+// amin == nullptr).
+hipError_t finish_sample(const float* x, const float* amin, const float* amax, float* action,
+                         int batch, int horizon, int action_dim, hipStream_t stream);
+
+}  // namespace fe::hip

@@ -1,0 +1,220 @@
+/*
+ * FlowEdge-compatible C ABI for the Diffusion Policy U-Net action head on AMD Instinct MI355X.
+ *
+ * Drop-in surface: every declaration below that carries a reference citation has the same name,
+ * argument meaning, status codes and thread-local error behaviour as elprofesoriqo/FlowEdge's
+ * `src/core/api/engine.h` (cited as engine.h:line).  The library behind it keeps the model
+ * weights and all scratch in one device arena allocated at load, and runs each sampling call as
+ * one hipGraph replay of hand-written gfx950 kernels.  Host buffers are caller-owned float
+ * arrays; sample/action buffers use [horizon][action_dim] order.
+ *
+ * Extensions (no reference counterpart) are grouped at the end and say so.
+ */
+#ifndef FLOWEDGE_AMD_H
+#define FLOWEDGE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct FeEngine fe_engine;
+typedef struct FeWeights fe_weights;
+
+/* engine.h:16-21 */
+enum {
+  FE_SOLVER_EULER = 0,
+  FE_SOLVER_HEUN = 1,
+  FE_SOLVER_RK4 = 2,
+};
+
+/* engine.h:23-27 */
+enum {
+  FE_DIFFUSION_DDIM = 0,
+  FE_DIFFUSION_DDPM = 1,
+};
+
+/* protocol/contracts.h:10-30 */
+enum {
+  FE_PROTOCOL_VERSION = 1,
+  FE_MODEL_DIGEST_BYTES = 16,
+};
+enum {
+  FE_ARCH_UNKNOWN = 0,
+  FE_ARCH_DIFFUSION_HEAD = 4,
+};
+enum {
+  FE_PRECISION_UNKNOWN = 0,
+  FE_PRECISION_F32 = 1,
+  FE_PRECISION_BF16 = 2,
+  FE_PRECISION_MIXED = 3,
+};
+
+/* engine.h:29-43 */
+typedef struct fe_diffusion_metadata {
+  uint32_t struct_size;
+  uint32_t protocol_version;
+  uint32_t clip_sample;
+  uint32_t reserved;
+  uint64_t action_dim;
+  uint64_t condition_dim;
+  uint64_t horizon;
+  uint64_t action_steps;
+  uint64_t observation_steps;
+  uint64_t train_timesteps;
+  float clip_sample_range;
+  float reserved_float;
+} fe_diffusion_metadata;
+
+/* protocol/contracts.h:62-83 */
+typedef struct fe_model_digest {
+  uint8_t bytes[FE_MODEL_DIGEST_BYTES];
+} fe_model_digest;
+typedef struct fe_model_metadata {
+  uint32_t struct_size;
+  uint32_t protocol_version;
+  uint32_t architecture;
+  uint32_t precision;
+  fe_model_digest model_digest;
+  uint64_t d_model;
+  uint64_t n_layers;
+  uint64_t d_inner;
+  uint64_t d_state;
+  uint64_t d_conv;
+  uint64_t action_dim;
+  uint64_t condition_dim;
+  uint64_t decode_snapshot_bytes;
+} fe_model_metadata;
+
+/* engine.h:46-59 */
+enum {
+  FE_STATUS_OK = 0,
+  FE_STATUS_INVALID_ARGUMENT = 1,
+  FE_STATUS_RESOURCE_EXHAUSTED = 2,
+  FE_STATUS_TOKEN_OUT_OF_RANGE = 3,
+  FE_STATUS_UNSUPPORTED_MODEL = 4,
+  FE_STATUS_INVALID_SOLVER = 5,
+  FE_STATUS_NO_ACTIVE_OPERATION = 6,
+  FE_STATUS_STATE_UNAVAILABLE = 7,
+  FE_STATUS_CANCELLED = 8,
+  FE_STATUS_INCOMPATIBLE_STATE = 9,
+  FE_STATUS_CORRUPT_STATE = 10,
+};
+
+/* engine.h:63 — last error on this thread; valid until the next ABI call; never NULL. */
+const char* fe_engine_last_error(void);
+
+/* engine.h:71 — load a dp.* .safetensors checkpoint into one device arena; NULL on failure. */
+fe_engine* fe_engine_load(const char* path);
+
+/* engine.h:82 — `worker_threads` (0-8) is validated and reported; device execution uses none. */
+fe_engine* fe_engine_load_with_threads(const char* path, unsigned worker_threads);
+
+/* engine.h:85 — immutable host weight store shareable by several engines. */
+fe_weights* fe_weights_load(const char* path);
+
+/* engine.h:88 */
+size_t fe_weights_size_bytes(const fe_weights* weights);
+
+/* engine.h:91 */
+void fe_weights_free(fe_weights* weights);
+
+/* engine.h:94 — each engine owns its own device arena built from the shared host store. */
+fe_engine* fe_engine_create_from_weights(const fe_weights* weights, unsigned worker_threads);
+
+/* engine.h:97 */
+fe_engine* fe_engine_create_from_weights_auto(const fe_weights* weights);
+
+/* engine.h:218 */
+unsigned fe_engine_thread_count(const fe_engine* engine);
+
+/* engine.h:227 — 1 when the weights are device-resident (always, for a loaded engine). */
+int fe_engine_cuda_resident(const fe_engine* engine);
+
+/* engine.h:230 */
+int fe_engine_model_metadata(const fe_engine* engine, fe_model_metadata* metadata);
+
+/* engine.h:245 */
+size_t fe_engine_action_dim(const fe_engine* engine);
+
+/* engine.h:251 */
+size_t fe_engine_action_horizon(const fe_engine* engine);
+
+/* engine.h:254 */
+int fe_engine_diffusion_metadata(const fe_engine* engine, fe_diffusion_metadata* metadata);
+
+/* engine.h:261 */
+size_t fe_engine_condition_dim(const fe_engine* engine);
+
+/* engine.h:277-278 — DDIM/DDPM action chunk in original action units. */
+int fe_engine_sample_diffusion(fe_engine* engine, const float* condition, const float* noise,
+                               size_t steps, int scheduler, uint64_t seed, float* action);
+
+/* engine.h:281-283 — one U-Net pass in normalized action space (epsilon, or velocity for a
+ * flow checkpoint). */
+int fe_engine_diffusion_denoise(fe_engine* engine, const float* condition,
+                                const float* normalized_sample, float timestep,
+                                float* predicted_noise);
+
+/* engine.h:318-319 — flow-ODE sample.  Served by a U-Net checkpoint whose dp.meta[12] == 1
+ * (velocity field v(x,t|c), continuous t in [0,1]); `noise` and `action` hold
+ * [horizon][action_dim] values and the result is x(1) without unnormalisation, as the
+ * reference flow head returns it (flow.cc:321). */
+int fe_engine_sample_condition(fe_engine* engine, const float* condition, const float* noise,
+                               size_t steps, int method, float* action);
+
+/* engine.h:395 */
+void fe_engine_free(fe_engine* engine);
+
+/* ---------------------------------------------------------------------------------------------
+ * Extensions (no reference counterpart).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Batched DDIM/DDPM: equal to `batch` independent fe_engine_sample_diffusion calls with the same
+ * steps/scheduler/seed.  condition [batch][condition_dim], noise/action
+ * [batch][horizon][action_dim]. */
+int fe_engine_sample_diffusion_batch(fe_engine* engine, const float* condition,
+                                     const float* noise, size_t batch, size_t steps,
+                                     int scheduler, uint64_t seed, float* action);
+
+/* Batched flow-ODE sample for a velocity checkpoint (see fe_engine_sample_condition). */
+int fe_engine_sample_condition_batch(fe_engine* engine, const float* condition,
+                                     const float* noise, size_t batch, size_t steps, int method,
+                                     float* action);
+
+/* Batched single U-Net pass. */
+int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
+                                      const float* normalized_sample, size_t batch,
+                                      float timestep, float* predicted_noise);
+
+/* Device-resident variants: the pointers are device memory (hipMalloc) of the same shapes;
+ * nothing crosses PCIe.  `kind` 0 = DDIM/DDPM (`mode` = scheduler, `seed` used by DDPM),
+ * 1 = flow ODE (`mode` = solver method).  Completes before returning. */
+int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_dev,
+                            const float* noise_dev, size_t batch, size_t steps, int mode,
+                            uint64_t seed, float* action_dev);
+
+/* Build (capture and instantiate) the sampling graph for this shape ahead of the first call. */
+int fe_engine_prepare(fe_engine* engine, int kind, size_t batch, size_t steps, int mode);
+
+/* Largest batch the arena was sized for (FLOWEDGE_MAX_BATCH at load, default 256). */
+size_t fe_engine_max_batch(const fe_engine* engine);
+
+/* Bytes of the single device arena owned by the engine. */
+size_t fe_engine_device_bytes(const fe_engine* engine);
+
+/* Device allocations made by this library in this process (one arena per engine; a sampling
+ * call never allocates). */
+uint64_t fe_device_alloc_count(void);
+
+/* Device time in milliseconds of the most recent sampling graph replay (hipEvents around the
+ * graph launch on the engine's stream), or -1 if none. */
+float fe_engine_last_device_ms(const fe_engine* engine);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLOWEDGE_AMD_H */

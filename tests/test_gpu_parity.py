@@ -1,0 +1,250 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical inputs.
+
+Tolerances (written per test): fp32 checkpoints must match within max |err| <= 1e-4 in action
+units (action scale (max - min)/2 = 1 for the synthetic range [-1, 1]); BF16-weight checkpoints
+are held to the same 1e-4 here because the oracle runs on the identical BF16-rounded values
+(the contract bound for BF16 variants is 2e-2).  Batched calls must equal independent batch-1
+calls bit for bit.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import flowedge_amd
+import oracle
+from flowedge_amd import checkpoint as ck
+from tests import unet_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def say(msg: str):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def tiny(ckpt_dir):
+    return ck.cached_checkpoint("tiny", ckpt_dir)
+
+
+@pytest.fixture(scope="module")
+def tiny_engine(tiny):
+    with flowedge_amd.Engine(tiny) as e:
+        yield e
+
+
+@pytest.fixture(scope="module")
+def tiny_oracle(tiny):
+    return oracle.Oracle(tiny)
+
+
+def maxerr(a, b) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+@pytest.mark.parametrize("t", [99.0, 90.0, 50.0, 0.0, 0.3])
+def test_tiny_denoise(tiny_engine, tiny_oracle, t):
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec)
+    say(f"tiny denoise t={t}")
+    got = tiny_engine.diffusion_denoise(cond[0], noise[0], t)
+    want = tiny_oracle.denoise(cond[0], noise[0], t)
+    assert maxerr(got, want) <= 2e-5
+
+
+@pytest.mark.parametrize("steps", [1, 3, 10, 100])
+def test_tiny_ddim(tiny_engine, tiny_oracle, steps):
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec)
+    say(f"tiny DDIM steps={steps}")
+    got = tiny_engine.sample_diffusion(cond[0], noise[0], steps=steps)
+    want = tiny_oracle.sample(cond[0], noise[0], steps)
+    assert maxerr(got, want) <= TOL
+    assert np.all(got >= -1.0) and np.all(got <= 1.0)
+
+
+@pytest.mark.parametrize("seed", [0, 42])
+def test_tiny_ddpm(tiny_engine, tiny_oracle, seed):
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec)
+    say(f"tiny DDPM seed={seed}")
+    got = tiny_engine.sample_diffusion(cond[0], noise[0], steps=10, scheduler="ddpm", seed=seed)
+    want = tiny_oracle.sample(cond[0], noise[0], 10, 1, seed)
+    assert maxerr(got, want) <= TOL
+    again = tiny_engine.sample_diffusion(cond[0], noise[0], steps=10, scheduler="ddpm", seed=seed)
+    assert np.array_equal(got, again)
+
+
+def test_tiny_ddim_seed_independent_and_repeatable(tiny_engine):
+    cond, noise = ck.inputs(ck.SPECS["tiny"])
+    a = tiny_engine.sample_diffusion(cond[0], noise[0], steps=10, seed=1)
+    b = tiny_engine.sample_diffusion(cond[0], noise[0], steps=10, seed=999)
+    assert np.array_equal(a, b)
+
+
+def test_tiny_batch_equals_independent_calls(tiny_engine):
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec, batch=5)
+    say("tiny DDIM batch=5")
+    batch = tiny_engine.sample_diffusion_batch(cond, noise, steps=10)
+    for b in range(5):
+        single = tiny_engine.sample_diffusion(cond[b], noise[b], steps=10)
+        assert np.array_equal(batch[b], single)
+    eps = tiny_engine.diffusion_denoise_batch(cond, noise, 50.0)
+    for b in range(5):
+        assert np.array_equal(eps[b], tiny_engine.diffusion_denoise(cond[b], noise[b], 50.0))
+
+
+def test_no_device_allocation_after_load(tiny_engine):
+    # core_model_tests.cc:475-495: device allocations do not change across sampling calls.
+    cond, noise = ck.inputs(ck.SPECS["tiny"], batch=3)
+    before = flowedge_amd.device_alloc_count()
+    assert before >= 1
+    tiny_engine.diffusion_denoise(cond[0], noise[0], 7.0)
+    tiny_engine.sample_diffusion(cond[0], noise[0], steps=5)
+    tiny_engine.sample_diffusion(cond[0], noise[0], steps=5, scheduler="ddpm", seed=42)
+    tiny_engine.sample_diffusion_batch(cond, noise, steps=5)
+    assert flowedge_amd.device_alloc_count() == before
+
+
+def test_status_codes(tiny_engine, tiny):
+    lib = flowedge_amd.lib()
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec)
+    out = np.empty((spec.horizon, spec.action_dim), np.float32)
+    p = flowedge_amd._p
+    c, n = np.ascontiguousarray(cond[0]), np.ascontiguousarray(noise[0])
+    h = tiny_engine._h
+    assert lib.fe_engine_sample_diffusion(h, p(c), p(n), 0, 0, 0, p(out)) == 1
+    assert lib.fe_engine_sample_diffusion(h, p(c), p(n), 101, 0, 0, p(out)) == 1
+    assert lib.fe_engine_sample_diffusion(h, p(c), p(n), 10, 7, 0, p(out)) == 5
+    assert lib.fe_engine_sample_condition(h, p(c), p(n), 10, 0, p(out)) == 4
+    assert lib.fe_engine_sample_diffusion(h, p(c), p(n), 10, 0, 0, p(out)) == 0
+    assert flowedge_amd.last_error() == ""
+    assert lib.fe_engine_diffusion_denoise(h, p(c), p(n), float("nan"), p(out)) == 1
+    big = tiny_engine.max_batch + 1
+    cb = np.zeros((big, spec.cond_dim), np.float32)
+    nb = np.zeros((big, spec.horizon, spec.action_dim), np.float32)
+    ob = np.empty_like(nb)
+    assert lib.fe_engine_sample_diffusion_batch(h, p(cb), p(nb), big, 10, 0, 0, p(ob)) == 1
+    md = tiny_engine.diffusion_metadata
+    assert (md["action_dim"], md["horizon"], md["condition_dim"], md["train_timesteps"]) == (
+        2, 16, 64, 100)
+    assert tiny_engine.model_metadata["architecture"] == 4
+    assert tiny_engine.cuda_resident
+
+
+def test_reference_fixture_model(ckpt_dir):
+    # The reference's own 2-stage fixture (kernel 3, groups 2, T=10, action range [-2,2]x[0,10]).
+    path = unet_ref.write_fixture(os.path.join(ckpt_dir, "ref_fixture.safetensors"))
+    o = oracle.Oracle(path)
+    say("reference fixture model")
+    with flowedge_amd.Engine(path) as e:
+        sample = unet_ref.seq(8, 0.23, -0.1)
+        cond = unet_ref.seq(3, 0.41, 0.2)
+        assert maxerr(e.diffusion_denoise(cond, sample, 7.0), o.denoise(cond, sample, 7.0)) <= 2e-6
+        cond = unet_ref.seq(3, 0.31, -0.2)
+        noise = unet_ref.seq(8, 0.29, 0.1)
+        ddim = e.sample_diffusion(cond, noise, steps=5)
+        assert maxerr(ddim, o.sample(cond, noise, 5, 0, 1)) <= 1e-5
+        ddpm = e.sample_diffusion(cond, noise, steps=5, scheduler="ddpm", seed=42)
+        assert maxerr(ddpm, o.sample(cond, noise, 5, 1, 42)) <= 1e-4
+        assert np.all(ddim[:, 0] >= -2) and np.all(ddim[:, 0] <= 2)
+        assert np.all(ddim[:, 1] >= 0) and np.all(ddim[:, 1] <= 10)
+
+
+@pytest.mark.parametrize("method,steps", [("euler", 10), ("heun", 3), ("rk4", 4)])
+def test_flow_unet_small(ckpt_dir, method, steps):
+    spec = ck.UNetSpec(dims=(64, 128, 256), action_dim=7, cond_dim=32, prediction=1)
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, "flow_small_gpu.safetensors"), spec)
+    o = oracle.Oracle(path)
+    cond, x0 = ck.inputs(spec, batch=3)
+    say(f"flow small {method} steps={steps}")
+    with flowedge_amd.Engine(path) as e:
+        out = np.empty((spec.horizon, spec.action_dim), np.float32)
+        e.sample_condition(cond[0], x0[0], out, steps=steps, method=method)
+        want = o.sample_flow(cond[0], x0[0], steps, flowedge_amd.SOLVERS[method])
+        assert maxerr(out, want) <= TOL
+        batch = e.sample_condition_batch(cond, x0, steps=steps, method=method)
+        assert np.array_equal(batch[0], out)
+        for b in (1, 2):
+            assert maxerr(batch[b], o.sample_flow(cond[b], x0[b], steps,
+                                                  flowedge_amd.SOLVERS[method])) <= TOL
+        with pytest.raises(RuntimeError):
+            e.sample_diffusion(cond[0], x0[0])
+
+
+def test_bf16_weights_small(ckpt_dir):
+    spec = ck.UNetSpec(dims=(64, 128, 256), horizon=8, action_dim=14, cond_dim=96,
+                       action_steps=4, bf16_weights=True)
+    path = ck.write_synthetic(os.path.join(ckpt_dir, "bf16_small.safetensors"), spec)
+    o = oracle.Oracle(path)
+    cond, noise = ck.inputs(spec, batch=2)
+    say("bf16 small")
+    with flowedge_amd.Engine(path) as e:
+        assert e.model_metadata["precision"] == 3
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+        for b in range(2):
+            assert maxerr(got[b], o.sample(cond[b], noise[b], 10)) <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# Full-size workloads.
+# ---------------------------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def pusht(ckpt_dir):
+    return ck.cached_checkpoint("pusht", ckpt_dir)
+
+
+def test_pusht_b1_ddim10_and_denoise(pusht):
+    spec = ck.SPECS["pusht"]
+    cond, noise = ck.inputs(spec)
+    o = oracle.Oracle(pusht, threads=8)
+    say("pusht B=1 DDIM-10")
+    with flowedge_amd.Engine(pusht) as e:
+        for t in (90.0, 0.0):
+            assert maxerr(e.diffusion_denoise(cond[0], noise[0], t),
+                          o.denoise(cond[0], noise[0], t)) <= 2e-5
+        got = e.sample_diffusion(cond[0], noise[0], steps=10)
+        err = maxerr(got, o.sample(cond[0], noise[0], 10))
+        say(f"pusht DDIM-10 max err {err:.3e}")
+        assert err <= TOL
+        cb, nb = ck.inputs(spec, batch=4)
+        batch = e.sample_diffusion_batch(cb, nb, steps=10)
+        assert np.array_equal(batch[0], got)
+        for b in range(1, 4):
+            assert np.array_equal(batch[b], e.sample_diffusion(cb[b], nb[b], steps=10))
+
+
+def test_bimanual_bf16(ckpt_dir):
+    spec = ck.SPECS["bimanual"]
+    path = ck.cached_checkpoint("bimanual", ckpt_dir)
+    o = oracle.Oracle(path, threads=8)
+    cond, noise = ck.inputs(spec, batch=2)
+    say("bimanual bf16 H=8 A=14")
+    with flowedge_amd.Engine(path) as e:
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+        for b in range(2):
+            assert maxerr(got[b], o.sample(cond[b], noise[b], 10)) <= TOL
+
+
+def test_flow_full_size(ckpt_dir):
+    spec = ck.SPECS["flow"]
+    path = ck.cached_checkpoint("flow", ckpt_dir)
+    o = oracle.Oracle(path, threads=8)
+    cond, x0 = ck.inputs(spec)
+    say("flow U-Net RK4-4 and Euler-10")
+    with flowedge_amd.Engine(path) as e:
+        for method, steps in (("rk4", 4), ("euler", 10)):
+            out = np.empty((spec.horizon, spec.action_dim), np.float32)
+            e.sample_condition(cond[0], x0[0], out, steps=steps, method=method)
+            want = o.sample_flow(cond[0], x0[0], steps, flowedge_amd.SOLVERS[method])
+            err = maxerr(out, want)
+            say(f"flow {method} max err {err:.3e}")
+            assert err <= TOL
