@@ -151,6 +151,7 @@ struct ConvSlot {
   const fe::TensorInfo* w_src = nullptr;
   const fe::TensorInfo* b_src = nullptr;
   bool transpose_storage = false;  // ConvTranspose1d [IC][OC][K]
+  bool force_f32 = false;          // widened to fp32 in the arena (read by the fused epilogue)
 };
 
 struct NormSlot {
@@ -261,7 +262,7 @@ struct Builder {
   std::string err;
 
   bool conv(const std::string& p, std::size_t oc, std::size_t ic, std::size_t k, int mode,
-            ConvSlot& s, bool transpose_storage = false) {
+            ConvSlot& s, bool transpose_storage = false, bool force_f32 = false) {
     const fe::TensorInfo* w = ck.find(p + ".w");
     const fe::TensorInfo* b = ck.find(p + ".b");
     if (w == nullptr || w->shape.size() != 3 || w->shape[0] != (transpose_storage ? ic : oc) ||
@@ -272,12 +273,13 @@ struct Builder {
     s.w_src = w;
     s.b_src = b;
     s.transpose_storage = transpose_storage;
-    s.op.bf16 = w->bf16;
+    s.force_f32 = force_f32;
+    s.op.bf16 = w->bf16 && !force_f32;
     s.op.mode = mode;
     s.op.k = static_cast<int>(k);
     s.op.ic = static_cast<int>(ic);
     s.op.oc = static_cast<int>(oc);
-    s.w_off = plan.take(w->elements() * (w->bf16 ? 2 : 4));
+    s.w_off = plan.take(w->elements() * (s.op.bf16 ? 2 : 4));
     s.b_off = plan.take(oc * 4);
     if (w->bf16) e.bf16_convs = true, e.any_bf16 = true;
     return true;
@@ -387,7 +389,7 @@ struct Builder {
     }
     if (!conv("dp.f.c", c.dims[0], c.dims[0], c.kernel, fe::hip::kConvSame, e.fconv) ||
         !norm("dp.f.n", c.dims[0], e.fnorm) ||
-        !conv("dp.f.o", c.action_dim, c.dims[0], 1, fe::hip::kConvSame, e.fout))
+        !conv("dp.f.o", c.action_dim, c.dims[0], 1, fe::hip::kConvSame, e.fout, false, true))
       return false;
     e.fconv.op.lin = e.fconv.op.lout = static_cast<int>(c.horizon);
     e.fout.op.lin = e.fout.op.lout = static_cast<int>(c.horizon);
@@ -483,14 +485,23 @@ void widen(const fe::TensorInfo* t, std::vector<float>& out) {
 hipError_t upload_conv(FeEngine& e, const ConvSlot& s) {
   const auto* w = s.w_src;
   const std::size_t oc = s.op.oc, ic = s.op.ic, k = s.op.k;
-  const std::size_t esz = w->bf16 ? 2 : 4;
+  const std::size_t src_esz = w->bf16 ? 2 : 4;
+  const std::size_t esz = s.op.bf16 ? 2 : 4;
   std::vector<char> packed(oc * ic * k * esz);
   const char* src = static_cast<const char*>(w->data);
   for (std::size_t o = 0; o < oc; ++o)
     for (std::size_t kk = 0; kk < k; ++kk)
       for (std::size_t i = 0; i < ic; ++i) {
         const std::size_t from = s.transpose_storage ? (i * oc + o) * k + kk : (o * ic + i) * k + kk;
-        std::memcpy(&packed[((o * k + kk) * ic + i) * esz], src + from * esz, esz);
+        char* dst = &packed[((o * k + kk) * ic + i) * esz];
+        if (esz == src_esz) {
+          std::memcpy(dst, src + from * src_esz, esz);
+        } else {  // BF16 -> F32
+          std::uint16_t bits;
+          std::memcpy(&bits, src + from * 2, 2);
+          const std::uint32_t wide = static_cast<std::uint32_t>(bits) << 16;
+          std::memcpy(dst, &wide, 4);
+        }
       }
   hipError_t st = upload(e.ptr<char>(s.w_off), packed.data(), packed.size());
   if (st != hipSuccess) return st;
@@ -737,7 +748,7 @@ hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int sche
   using namespace fe::hip;
   const Config& c = e.cfg;
   const std::size_t ratio = c.train_timesteps / steps;
-  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_state), batch,
+  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
   TimeSpec ts;
   ts.mode = kTimesDiffusion;
@@ -753,7 +764,7 @@ hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int sche
     const float bt = 1.0f - at;
     UpdateOp u{};
     u.x = e.ptr(e.x_state);
-    u.xin = e.ptr(e.x_state);
+    u.xin = e.ptr(e.x_in);
     u.sqrt_at = std::sqrt(at);
     u.sqrt_bt = std::sqrt(bt);
     u.clip = c.clip ? 1 : 0;
@@ -776,7 +787,6 @@ hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int sche
       if (prev >= 0) ++noisy_steps;
     }
     const float* row = e.ptr(e.film_table) + i * e.film_total;
-    // DDIM and DDPM read xin == x: the state is the U-Net input.
     FE_TRY(enqueue_unet(e, batch, row, u));
   }
   return finish_sample(e.ptr(e.x_state), e.ptr(e.amin), e.ptr(e.amax), e.ptr(e.out_action), batch,
