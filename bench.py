@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""Benchmark of the Diffusion Policy U-Net sampling tick on one MI355X.
+
+Headline (``value``): p50 latency of one sampling tick -- 10-step DDIM of the LeRobot
+diffusion_pusht-size Conv1D U-Net (widths 512/1024/2048, horizon 16, action_dim 2, condition
+132, fp32) at batch 1 -- with condition and noise already resident in HBM.  A "step" of this
+benchmark is one tick.  Also reported: host-to-host p50/p99 through the host-pointer ABI
+(PCIe-inclusive, never ``value``), actions/sec at batch 256, the HBM roofline of the tick, and the
+CPU oracle timed on this host's cores.
+
+Roofline: algorithmic bytes of a tick = all U-Net weights once per U-Net evaluation
+(1,006,026,968 bytes x 10 = 10.06 GB); ``achieved`` = those bytes / the device time of one
+sampling-graph replay (hipEvents recorded on the engine's stream around the replay).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+METRIC = "p50 tick latency (B=1, 10-step DDIM) + actions/sec at B=256, % roofline"
+
+
+def unet_bytes_and_flops(spec, batch: int = 1):
+    """Algorithmic bytes (each weight once) and FLOPs of one U-Net evaluation."""
+    from flowedge_amd import checkpoint as ck
+
+    weight_bytes = 0
+    flops = 0
+    H = spec.horizon
+    dims = list(spec.dims)
+    for name, shape, kind, _ in ck.layout(spec):
+        n = 1
+        for s in shape:
+            n *= s
+        esize = 2 if (spec.bf16_weights and kind == "w") else 4
+        weight_bytes += n * esize
+    weight_bytes += (2 * spec.action_dim + 16 + len(dims)) * 4  # action range, meta, dims
+
+    def conv_f(oc, ic, k, lout):
+        return 2 * oc * ic * k * lout
+
+    L = H
+    for s, oc in enumerate(dims):
+        ic = spec.action_dim if s == 0 else dims[s - 1]
+        for blk in range(2):
+            cin = ic if blk == 0 else oc
+            flops += conv_f(oc, cin, spec.kernel, L) + conv_f(oc, oc, spec.kernel, L)
+            flops += 2 * (2 * oc) * (spec.timestep_dim + spec.cond_dim)
+            if cin != oc:
+                flops += conv_f(oc, cin, 1, L)
+        if s + 1 < len(dims):
+            flops += conv_f(oc, oc, 3, L // 2)
+            L //= 2
+    for _ in range(2):
+        flops += 2 * conv_f(dims[-1], dims[-1], spec.kernel, L) + 2 * 2 * dims[-1] * (
+            spec.timestep_dim + spec.cond_dim)
+    for u in range(len(dims) - 1):
+        high, low = dims[-1 - u], dims[-2 - u]
+        flops += conv_f(low, 2 * high, spec.kernel, L) + conv_f(low, 2 * high, 1, L)
+        flops += 3 * conv_f(low, low, spec.kernel, L) + 2 * 2 * (2 * low) * (
+            spec.timestep_dim + spec.cond_dim)
+        flops += 2 * low * low * 4 * L  # ConvTranspose K4 over L inputs
+        L *= 2
+    flops += conv_f(dims[0], dims[0], spec.kernel, H) + conv_f(spec.action_dim, dims[0], 1, H)
+    return weight_bytes, flops * batch
+
+
+def percentile(xs, q):
+    import numpy as np
+
+    return float(np.percentile(np.asarray(xs, dtype=np.float64), q))
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(path, spec, budget_s: float):
+    """The CPU oracle (this repository's C++ restatement of the reference CPU path) on the host:
+    caller-thread-only and all-cores p50 of a bounded number of full ticks."""
+    import numpy as np
+
+    import oracle
+    from flowedge_amd import checkpoint as ck
+
+    cond, noise = ck.inputs(spec)
+    out = {}
+    for label, threads in (("threads1", 0), ("all_cores", os.cpu_count() or 1)):
+        o = oracle.Oracle(path, threads=threads if threads > 1 else 0)
+        o.sample(cond[0], noise[0], 10)  # warmup (first-touch of the weights)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 20 and (time.perf_counter() - t_start) < budget_s / 2:
+            t0 = time.perf_counter()
+            o.sample(cond[0], noise[0], 10)
+            times.append((time.perf_counter() - t0) * 1e3)
+        o.close()
+        out[label] = {"p50_ms": percentile(times, 50), "ticks": len(times),
+                      "cores": max(threads, 1)}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed ticks")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="pusht")
+    ap.add_argument("--large-batch", type=int, default=256)
+    ap.add_argument("--large-steps", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported by this build "
+              "(the Diffusion Policy tick is measured on a single MI355X).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import flowedge_amd
+    from flowedge_amd import checkpoint as ck
+
+    spec = ck.SPECS[args.workload]
+    path = ck.cached_checkpoint(args.workload)
+    print(f"[bench] checkpoint {path}", file=sys.stderr, flush=True)
+    wbytes, nfe_flops = unet_bytes_and_flops(spec)
+    steps_ddim = 10
+    tick_bytes = wbytes * steps_ddim
+
+    eng = flowedge_amd.Engine(path)
+    dev = torch.device("cuda:0")
+    cond, noise = ck.inputs(spec, batch=1)
+    d_cond = torch.from_numpy(cond).to(dev)
+    d_noise = torch.from_numpy(noise).to(dev)
+    d_out = torch.empty((1, spec.horizon, spec.action_dim), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    eng.prepare(0, 1, steps_ddim, 0)
+
+    def tick(b, c, n, o):
+        eng.sample_device(0, c.data_ptr(), n.data_ptr(), b, steps_ddim, 0, 0, o.data_ptr())
+
+    for _ in range(args.warmup):
+        tick(1, d_cond, d_noise, d_out)
+    torch.cuda.synchronize()
+    lat, devms = [], []
+    t_all = time.perf_counter()
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        tick(1, d_cond, d_noise, d_out)
+        lat.append((time.perf_counter() - t0) * 1e3)
+        devms.append(eng.last_device_ms)
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - t_all) * 1e3
+    p50 = percentile(lat, 50)
+    dev_p50 = percentile(devms, 50)
+    print(f"[bench] B=1 DDIM-10 tick p50 {p50:.3f} ms (device {dev_p50:.3f} ms)", file=sys.stderr,
+          flush=True)
+
+    # Host-to-host (PCIe-inclusive) through the reference-shaped ABI.
+    host = []
+    for i in range(min(args.steps, 100)):
+        t0 = time.perf_counter()
+        eng.sample_diffusion(cond[0], noise[0], steps=steps_ddim)
+        host.append((time.perf_counter() - t0) * 1e3)
+    host_p50, host_p99 = percentile(host[5:], 50), percentile(host[5:], 99)
+
+    # Parity of the timed path against the oracle is covered by tests; report the action norm.
+    action = d_out.cpu().numpy()
+
+    # Large batch.
+    large = None
+    B = args.large_batch
+    if B > 0:
+        cb, nb = ck.inputs(spec, batch=B)
+        d_cb = torch.from_numpy(cb).to(dev)
+        d_nb = torch.from_numpy(nb).to(dev)
+        d_ob = torch.empty((B, spec.horizon, spec.action_dim), dtype=torch.float32, device=dev)
+        eng.prepare(0, B, steps_ddim, 0)
+        tick(B, d_cb, d_nb, d_ob)
+        torch.cuda.synchronize()
+        bl, bd = [], []
+        for _ in range(args.large_steps):
+            t0 = time.perf_counter()
+            tick(B, d_cb, d_nb, d_ob)
+            bl.append((time.perf_counter() - t0) * 1e3)
+            bd.append(eng.last_device_ms)
+        bp50 = percentile(bl, 50)
+        flops_tick = nfe_flops * B * steps_ddim
+        large = {
+            "batch": B, "p50_ms": bp50, "device_p50_ms": percentile(bd, 50),
+            "actions_per_sec": B * spec.horizon / (bp50 / 1e3),
+            "chunks_per_sec": B / (bp50 / 1e3),
+            "tflops": flops_tick / (percentile(bd, 50) / 1e3) / 1e12,
+            "mfma_peak_tflops": FP32_MFMA_PEAK_TFLOPS,
+        }
+        large["frac_of_fp32_mfma_peak"] = large["tflops"] / FP32_MFMA_PEAK_TFLOPS
+        print(f"[bench] B={B} DDIM-10 tick p50 {bp50:.2f} ms", file=sys.stderr, flush=True)
+
+    achieved = tick_bytes / (dev_p50 / 1e3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(p50, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(p50 / 810.0, 6),
+        "vs_baseline_note": "value / 810 ms (reference native 10-step DDIM p50, caller thread, "
+                            "docs/performance.md:59-64); lower is better",
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "LeRobot diffusion_pusht-size ConditionalUnet1D, DDIM 10 steps, batch 1",
+            "dims": list(spec.dims), "horizon": spec.horizon, "action_dim": spec.action_dim,
+            "cond_dim": spec.cond_dim, "kernel": spec.kernel, "groups": spec.groups,
+            "train_timesteps": spec.train_timesteps, "batch": 1, "inference_steps": steps_ddim,
+            "inputs": "device-resident (fe_engine_sample_device)",
+        },
+        "p99_ms": round(percentile(lat, 99), 4),
+        "device_p50_ms": round(dev_p50, 4),
+        "host_to_host_p50_ms": round(host_p50, 4),
+        "host_to_host_p99_ms": round(host_p99, 4),
+        "actions_per_sec_b1": round(spec.horizon / (p50 / 1e3), 1),
+        "actions_per_sec_definition": "batch * horizon / p50 tick seconds",
+        "large_batch": large,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "sampling tick (one hipGraph replay: 10 U-Net evaluations + updates)",
+            "algorithmic_bytes_per_launch": tick_bytes,
+        },
+        "finite": bool(np.all(np.isfinite(action))),
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(path, spec, args.cpu_budget)
+        result["cpu_baseline"] = {
+            "value": round(cb["threads1"]["p50_ms"], 2),
+            "unit": "ms",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{cb['threads1']['ticks']} full B=1 DDIM-10 ticks, caller thread only",
+            "all_cores": {"value": round(cb["all_cores"]["p50_ms"], 2),
+                          "cores": cb["all_cores"]["cores"],
+                          "ticks": cb["all_cores"]["ticks"]},
+            "cpu_model": cpu_model(),
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

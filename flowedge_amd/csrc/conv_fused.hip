@@ -1,0 +1,125 @@
+// Host side of the fused convolution: launch planning and dispatch to the kernel instances
+// (conv_kernel.h describes the kernel).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "conv_kernel.h"
+#include "kernels.h"
+
+namespace fe::hip {
+namespace {
+
+using namespace conv;
+
+struct LaunchPlan {
+  int vec = 4;
+  int tpr = 64;
+  int nch = 1;
+  int tiles = 0;
+  int blocks = 0;
+};
+
+bool lin_ok(int lin) { return lin == 1 || lin == 2 || lin == 4 || lin == 8 || lin == 16; }
+
+// Lanes per row and chunks per lane: the fewest lanes per row (most rows per tile) whose chunk
+// count fits the register budget while leaving at least one row tile per CU; shapes with fewer
+// rows take the lane count with the most tiles.  Tiles are then spread evenly over at most one
+// workgroup per CU.
+bool plan_conv(const ConvOp& op, bool res, int split, bool norm, LaunchPlan& p) {
+  if (!lin_ok(op.lin) || op.ic <= 0 || op.oc <= 0 || split <= 0 || split > op.ic) return false;
+  if (op.mode == kConvSame) {
+    if (op.k != 3 && op.k != 5) return false;
+  } else if (op.mode == kConvDown) {
+    if (op.k != 3 || op.lin < 2 || res) return false;
+  } else if (op.mode == kConvTranspose) {
+    if (op.k != 4 || res) return false;
+  } else {
+    return false;
+  }
+  if (op.lout != lout_of(op.mode, op.lin)) return false;
+  p.vec = (op.ic % 4 == 0 && split % 4 == 0) ? 4 : 1;
+  if (p.vec == 1 && (norm || op.mode != kConvSame)) return false;
+  if (op.ic * op.lin > kMaxStageFloats) return false;
+  if (norm && split * op.lin > kMaxNormFloats) return false;
+  const int nv = op.ic / p.vec;
+  const int budget = chunk_budget(op.k, op.lin, res, p.vec);
+  int best = -1, best_tiles = 0;
+  for (int tpr = kWave; tpr <= kThreads; tpr *= 2) {
+    const int nch = (nv + tpr - 1) / tpr;
+    if (nch > budget) continue;
+    const int rpt = kThreads / tpr;
+    const int tiles = (op.oc + rpt - 1) / rpt;
+    if (tiles >= kMaxBlocks) {
+      best = tpr;
+      break;
+    }
+    if (tiles > best_tiles) {
+      best = tpr;
+      best_tiles = tiles;
+    }
+  }
+  if (best < 0) return false;
+  p.tpr = best;
+  p.nch = (nv + best - 1) / best;
+  p.tiles = (op.oc + kThreads / best - 1) / (kThreads / best);
+  const int per = (p.tiles + kMaxBlocks - 1) / kMaxBlocks;  // tiles per workgroup
+  p.blocks = (p.tiles + per - 1) / per;
+  return true;
+}
+
+int prologue_of(const ConvInput& in) {
+  if (!in.norm) return kProPlain;
+  if (in.film_time != nullptr && in.res == nullptr) return kProFilm;
+  if (in.film_time == nullptr && in.res != nullptr) return kProResid;
+  return -1;
+}
+
+}  // namespace
+
+bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm) {
+  LaunchPlan p;
+  return plan_conv(op, res1x1, split, norm, p);
+}
+
+hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
+                      View yr, int batch, hipStream_t stream) {
+  const bool res = res1x1 != nullptr;
+  LaunchPlan p;
+  if (!plan_conv(op, res, in.split, in.norm, p)) return hipErrorInvalidValue;
+  const int pro = prologue_of(in);
+  if (pro < 0) return hipErrorInvalidValue;
+  if (in.norm && (in.groups <= 0 || in.groups > kMaxGroups || in.split % in.groups != 0 ||
+                  (in.split / in.groups * op.lin) % 4 != 0))
+    return hipErrorInvalidValue;
+  if (in.split < op.ic && in.plain == nullptr) return hipErrorInvalidValue;
+  if (res && (res1x1->k != 1 || res1x1->ic != op.ic || res1x1->oc != op.oc || yr.p == nullptr))
+    return hipErrorInvalidValue;
+  if (batch <= 0 || batch > 65535) return hipErrorInvalidValue;
+  Args a{};
+  a.w = op.w;
+  a.bias = op.b;
+  a.y = y.p;
+  a.ys = y.stride;
+  a.bf16 = op.bf16 ? 1 : 0;
+  if (res) {
+    a.rw = res1x1->w;
+    a.rbias = res1x1->b;
+    a.yr = yr.p;
+    a.yrs = yr.stride;
+    a.rbf16 = res1x1->bf16 ? 1 : 0;
+  }
+  a.oc = op.oc;
+  a.ic = op.ic;
+  a.tiles = p.tiles;
+  a.blocks = p.blocks;
+  a.tpr = p.tpr;
+  a.nch = p.nch;
+  a.in = in;
+  if (op.mode == kConvSame)
+    return op.k == 5 ? launch_same5(op.lin, p.vec, pro, res, a, batch, stream)
+                     : launch_same3(op.lin, p.vec, pro, res, a, batch, stream);
+  return launch_resample(op.mode, op.lin, pro, a, batch, stream);
+}
+
+}  // namespace fe::hip

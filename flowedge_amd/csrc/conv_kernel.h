@@ -1,0 +1,540 @@
+// Fused weight-streaming convolution for the Diffusion Policy U-Net on gfx950 (device template).
+//
+// One launch computes a Conv1d (kernel 3/5 "same", the K=3 stride-2 conv of Downsample1d, or the
+// K=4 stride-2 ConvTranspose1d of Upsample1d) of one sample per grid row, optionally together with
+// the ResidualBlock's 1x1 projection of the same input (as an extra tap with its own outputs).
+// Weights are stored [OC][K][IC] (repacked at load), so the lanes of a row group stream
+// consecutive 16-byte vectors of one (oc, tap) row.
+//
+// Work split: 512-lane workgroups, at most one per CU (two wavefronts per SIMD, so up to 256
+// VGPRs per lane hold the weights in flight).  A workgroup
+//   1. requests its share of the input (raw producer output, residual, GroupNorm/FiLM parameters)
+//      into registers,
+//   2. then requests every weight vector of its first row tile (up to 160 floats per lane), so the
+//      input arrives first and the weights keep streaming during the prologue,
+//   3. computes the GroupNorm statistics of the sample (fp64 partials, var = E[x^2] - mean^2 as
+//      group_norm, diffusion_ops.cc:270-350), applies GN + Mish (+ FiLM) (+ residual), writes its
+//      share of the result out for ops that read it again ("materialises" it), and stages the
+//      whole input in LDS, channel-swizzled so row-group reads are bank-conflict free,
+//   4. walks its row tiles: as each input chunk's products are accumulated, the registers that
+//      held its weights are refilled with the next tile's, then partial sums are folded with a
+//      wavefront reduce-scatter (and across wavefronts through LDS when a row spans several).
+// Barriers inside the kernel order LDS only; weight loads stay in flight across them.
+//
+// Reference semantics: conv1d diffusion_ops.cc:82-163, conv_transpose1d :165-268, film :352-377,
+// ResidualBlock diffusion.cc:724-773.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace fe::hip::conv {
+
+using namespace dev;
+
+constexpr int kThreads = 512;
+constexpr int kMaxStageFloats = 16384;  // staged input per sample: channels * positions (64 KB)
+constexpr int kMaxNormFloats = 8192;    // of which normalised (GroupNorm prologue)
+constexpr int kMaxGroups = 32;
+constexpr int kWeightRegs = 160;        // weight floats in flight per lane
+constexpr int kMaxBlocks = 256;         // one workgroup per CU
+
+// Input prologue kinds (the only ones the U-Net produces).
+enum Prologue : int {
+  kProPlain = 0,  // raw tensor(s)
+  kProFilm = 1,   // FiLM(mish(GN(src)))            (ResidualBlock conv2 input)
+  kProResid = 2,  // mish(GN(src)) + res, then plain (ResidualBlock output, maybe with a skip)
+};
+
+__host__ __device__ constexpr int lout_of(int mode, int lin) {
+  return mode == kConvSame ? lin : (mode == kConvDown ? lin / 2 : 2 * lin);
+}
+
+// Input chunks (VEC channels each) a lane handles per row: bounded by the weight registers (fewer
+// at LIN >= 8, where the chunk's input vectors take more), by what the largest staged input needs
+// at 64 lanes per row, and by 8.
+__host__ __device__ constexpr int chunk_budget(int k, int lin, bool res, int vec) {
+  const int taps = k + (res ? 1 : 0);
+  const int regs = lin >= 8 ? kWeightRegs - 32 : kWeightRegs;
+  const int by_regs = regs / (taps * vec);
+  const int by_size = (kMaxStageFloats / (lin * vec) + 63) / 64;
+  const int n = by_regs < by_size ? by_regs : by_size;
+  return n < 8 ? n : 8;
+}
+
+struct Args {
+  const void* w;       // [oc][K][ic]
+  const float* bias;   // [oc]
+  float* y;            // [B][oc][lout]
+  std::int64_t ys;
+  const void* rw;      // fused 1x1 projection [oc][ic] (RES)
+  const float* rbias;
+  float* yr;
+  std::int64_t yrs;
+  int bf16, rbf16;
+  int oc, ic;
+  int tiles;   // row tiles of kThreads / tpr rows
+  int blocks;  // workgroups (grid.x); workgroup g takes tiles g, g + blocks, ...
+  int tpr;     // lanes per row
+  int nch;     // chunks per lane (<= chunk_budget)
+  ConvInput in;
+};
+
+// Workgroup barrier that orders LDS accesses only: global loads in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() { __barrier(__CLK_LOCAL_MEM_FENCE); }
+
+// Input index read by output t through tap k, or -1 when it falls in the zero padding.
+template <int MODE, int K, int LIN>
+__device__ __forceinline__ constexpr int src_index(int t, int k) {
+  if constexpr (MODE == kConvSame) {
+    const int j = t + k - K / 2;
+    return (j >= 0 && j < LIN) ? j : -1;
+  } else if constexpr (MODE == kConvDown) {
+    const int j = 2 * t + k - 1;
+    return (j >= 0 && j < LIN) ? j : -1;
+  } else {
+    // ConvTranspose: output ot = 2 * it + k - 1.
+    const int num = t + 1 - k;
+    if (num < 0 || (num & 1)) return -1;
+    const int j = num / 2;
+    return j < LIN ? j : -1;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_w(const void* base, int bf16, std::int64_t idx, float* out) {
+  if (bf16) {
+    const unsigned short* p = static_cast<const unsigned short*>(base) + idx;
+    if constexpr (VEC == 4) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(p);
+      out[0] = __uint_as_float(raw.x << 16);
+      out[1] = __uint_as_float(raw.x & 0xffff0000u);
+      out[2] = __uint_as_float(raw.y << 16);
+      out[3] = __uint_as_float(raw.y & 0xffff0000u);
+    } else {
+      out[0] = bf16_to_f32(*p);
+    }
+  } else {
+    const float* p = static_cast<const float*>(base) + idx;
+    if constexpr (VEC == 4) {
+      const float4 v = *reinterpret_cast<const float4*>(p);
+      out[0] = v.x;
+      out[1] = v.y;
+      out[2] = v.z;
+      out[3] = v.w;
+    } else {
+      out[0] = *p;
+    }
+  }
+}
+
+// Weights of one input chunk (all taps, then the projection tap) of one row.
+template <int K, int VEC, bool RES>
+__device__ __forceinline__ void load_chunk(const Args& a, int row, int cv, bool valid,
+                                           float (&w)[K + (RES ? 1 : 0)][VEC]) {
+  if (valid) {
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      load_w<VEC>(a.w, a.bf16, (static_cast<std::int64_t>(row) * K + k) * a.ic + cv * VEC, w[k]);
+    if constexpr (RES)
+      load_w<VEC>(a.rw, a.rbf16, static_cast<std::int64_t>(row) * a.ic + cv * VEC, w[K]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K + (RES ? 1 : 0); ++k)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) w[k][v] = 0.0f;
+  }
+}
+
+// LDS layout of the staged input: channel c = 4 cv + v, position t lives at
+//   ((v * NPB + t / P) * nv + cv) * P + t % P,   P = min(LIN, 4), NPB = LIN / P,
+// so for fixed (v, t / P) the lanes of a row group (consecutive cv) read consecutive P-float
+// vectors.
+template <int LIN>
+struct Swz {
+  static constexpr int P = LIN >= 4 ? 4 : LIN;
+  static constexpr int NPB = LIN / P;
+  __device__ static __forceinline__ int at(int c, int t, int nv) {
+    return (((c & 3) * NPB + t / P) * nv + (c >> 2)) * P + t % P;
+  }
+};
+
+template <int LIN, int PRO>
+struct StageRegs {
+  static constexpr int QMAX = (kMaxStageFloats / 4 + kThreads - 1) / kThreads;
+  static constexpr int QN = PRO == kProPlain ? 1 : (kMaxNormFloats / 4 + kThreads - 1) / kThreads;
+  static constexpr int QP = LIN >= 4 ? QN : 1;  // per-chunk parameters (one channel per chunk)
+  float4 x[QMAX];
+  float4 r[PRO == kProResid ? QN : 1];
+  float gam[QP], bet[QP];
+  float ts[PRO == kProFilm ? QP : 1], cs[PRO == kProFilm ? QP : 1];
+  float tb[PRO == kProFilm ? QP : 1], cb[PRO == kProFilm ? QP : 1];
+};
+
+// Step 1: every global read of the prologue, issued before any weight load.  Lane `tid` takes the
+// float4 chunks q = tid + m * kThreads of the flat [C][L] input; chunks q < nqn come from `src`.
+template <int LIN, int PRO>
+__device__ __forceinline__ void stage_issue(const Args& a, int b, StageRegs<LIN, PRO>& s) {
+  using S = StageRegs<LIN, PRO>;
+  const ConvInput& in = a.in;
+  const int nq = a.ic * LIN / 4;
+  const int nqn = in.split * LIN / 4;
+  const int tid = threadIdx.x;
+  const float* src = in.src + b * in.src_stride;
+#pragma unroll
+  for (int m = 0; m < S::QMAX; ++m) {
+    const int q = tid + m * kThreads;
+    s.x[m] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (q < nq) {
+      const float* p = q < nqn ? src + 4 * q : in.plain + b * in.plain_stride + 4 * (q - nqn);
+      s.x[m] = *reinterpret_cast<const float4*>(p);
+    }
+  }
+  if constexpr (PRO != kProPlain) {
+#pragma unroll
+    for (int m = 0; m < S::QN; ++m) {
+      const int q = tid + m * kThreads;
+      if (q < nqn) {
+        if constexpr (PRO == kProResid)
+          s.r[m] = *reinterpret_cast<const float4*>(in.res + b * in.res_stride + 4 * q);
+        if constexpr (LIN >= 4) {
+          const int c = 4 * q / LIN;
+          s.gam[m] = in.gamma[c];
+          s.bet[m] = in.beta[c];
+          if constexpr (PRO == kProFilm) {
+            const float* ft = in.film_time + in.film_off;
+            const float* fc = in.film_cond + b * in.film_cond_stride + in.film_off;
+            s.ts[m] = ft[c];
+            s.cs[m] = fc[c];
+            s.tb[m] = ft[in.split + c];
+            s.cb[m] = fc[in.split + c];
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int LIN>
+__device__ __forceinline__ void write_chunk(float* xs, int nv, int q, float4 v) {
+  const int e = 4 * q;
+  if constexpr (LIN >= 4) {
+    *reinterpret_cast<float4*>(xs + Swz<LIN>::at(e / LIN, e % LIN, nv)) = v;
+  } else if constexpr (LIN == 2) {
+    *reinterpret_cast<float2*>(xs + Swz<2>::at(e / 2, 0, nv)) = float2{v.x, v.y};
+    *reinterpret_cast<float2*>(xs + Swz<2>::at(e / 2 + 1, 0, nv)) = float2{v.z, v.w};
+  } else {
+    xs[Swz<1>::at(e, 0, nv)] = v.x;
+    xs[Swz<1>::at(e + 1, 0, nv)] = v.y;
+    xs[Swz<1>::at(e + 2, 0, nv)] = v.z;
+    xs[Swz<1>::at(e + 3, 0, nv)] = v.w;
+  }
+}
+
+// Steps 3: statistics, transform, materialisation and LDS staging.  Called by every lane.
+template <int LIN, int PRO>
+__device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, StageRegs<LIN, PRO>& s,
+                                             float* xs, float* gmean, float* ginv) {
+  using S = StageRegs<LIN, PRO>;
+  const ConvInput& in = a.in;
+  const int nq = a.ic * LIN / 4;
+  const int nv = a.ic / 4;
+  const int tid = threadIdx.x;
+  if constexpr (PRO != kProPlain) {
+    const int nqn = in.split * LIN / 4;
+    const int npg = in.split / in.groups * LIN / 4;  // chunks per group
+    // fp64 partial sums per chunk, aliased over xs (written only after the next two barriers).
+    double* ps = reinterpret_cast<double*>(xs);
+    double* pq = ps + nqn;
+#pragma unroll
+    for (int m = 0; m < S::QN; ++m) {
+      const int q = tid + m * kThreads;
+      if (q < nqn) {
+        const double d0 = s.x[m].x, d1 = s.x[m].y, d2 = s.x[m].z, d3 = s.x[m].w;
+        ps[q] = (d0 + d1) + (d2 + d3);
+        pq[q] = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+      }
+    }
+    lds_barrier();
+    const int wave = tid / kWave, lane = tid & (kWave - 1);
+    for (int g = wave; g < in.groups; g += kThreads / kWave) {
+      double sum = 0.0, sq = 0.0;
+      for (int i = lane; i < npg; i += kWave) {
+        sum += ps[g * npg + i];
+        sq += pq[g * npg + i];
+      }
+      sum = wave_sum(sum);
+      sq = wave_sum(sq);
+      if (lane == 0) {
+        const double n = 4.0 * npg;
+        const double mean = sum / n;
+        const double var = fmax(0.0, sq / n - mean * mean);
+        gmean[g] = static_cast<float>(mean);
+        ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
+      }
+    }
+    lds_barrier();  // statistics visible; the partials are no longer read
+    const float* ft = PRO == kProFilm ? in.film_time + in.film_off : nullptr;
+    const float* fc = PRO == kProFilm ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
+#pragma unroll
+    for (int m = 0; m < S::QN; ++m) {
+      const int q = tid + m * kThreads;
+      if (q < nqn) {
+        const int g = q / npg;
+        const float mean = gmean[g], inv = ginv[g];
+        float v[4] = {s.x[m].x, s.x[m].y, s.x[m].z, s.x[m].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float gm, bt, sc = 0.0f, sh = 0.0f;
+          if constexpr (LIN >= 4) {
+            gm = s.gam[m];
+            bt = s.bet[m];
+            if constexpr (PRO == kProFilm) {
+              sc = s.ts[m] + s.cs[m];
+              sh = s.tb[m] + s.cb[m];
+            }
+          } else {
+            const int c = (4 * q + i) / LIN;
+            gm = in.gamma[c];
+            bt = in.beta[c];
+            if constexpr (PRO == kProFilm) {
+              sc = ft[c] + fc[c];
+              sh = ft[in.split + c] + fc[in.split + c];
+            }
+          }
+          float val = mish_fast(fmaf(v[i] - mean, inv * gm, bt));
+          if constexpr (PRO == kProFilm) val = fmaf(sc, val, sh);
+          v[i] = val;
+        }
+        if constexpr (PRO == kProResid) {
+          v[0] += s.r[m].x;
+          v[1] += s.r[m].y;
+          v[2] += s.r[m].z;
+          v[3] += s.r[m].w;
+        }
+        s.x[m] = float4{v[0], v[1], v[2], v[3]};
+        if (in.mat != nullptr && q % a.blocks == wg)
+          *reinterpret_cast<float4*>(in.mat + b * in.mat_stride + 4 * q) = s.x[m];
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < S::QMAX; ++m) {
+    const int q = tid + m * kThreads;
+    if (q < nq) write_chunk<LIN>(xs, nv, q, s.x[m]);
+  }
+  lds_barrier();
+}
+
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
+__global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
+  constexpr int LOUT = lout_of(MODE, LIN);
+  constexpr int TAPS = K + (RES ? 1 : 0);
+  constexpr int NCH = chunk_budget(K, LIN, RES, VEC);
+  constexpr int V = RES ? 2 * LOUT : LOUT;
+  static_assert(V <= kWave, "one reduced value per lane");
+  extern __shared__ float4 xs4[];
+  float* xs = reinterpret_cast<float*>(xs4);
+  __shared__ float gmean[kMaxGroups], ginv[kMaxGroups];
+  __shared__ float red[2 * (kThreads / kWave) * V];
+  const int tid = threadIdx.x;
+  const int wg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int rpt = kThreads / a.tpr;  // rows per tile
+  const int gid = tid / a.tpr;
+  const int lg = tid - gid * a.tpr;
+  const int nv = a.ic / VEC;
+  const int lane = tid & (kWave - 1);
+
+  StageRegs<LIN, PRO> st;
+  if constexpr (VEC == 4) stage_issue<LIN, PRO>(a, b, st);
+  __builtin_amdgcn_sched_barrier(0);  // the prologue's reads go out before the weights
+  int tile = wg;
+  float w[NCH][TAPS][VEC];
+  {
+    const int row = tile * rpt + gid;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int cv = lg + j * a.tpr;
+      if (j < a.nch) load_chunk<K, VEC, RES>(a, row, cv, cv < nv && row < a.oc, w[j]);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (VEC == 4) stage_finish<LIN, PRO>(a, b, wg, st, xs, gmean, ginv);
+
+  const int waves = a.tpr / kWave;
+  const int wig = lg / kWave;
+  const float* xsrc = a.in.src + b * a.in.src_stride;
+  int parity = 0;
+  for (; tile < a.tiles; tile += a.blocks) {
+    const int row = tile * rpt + gid;
+    const int next = tile + a.blocks;
+    const bool more = next < a.tiles;
+    const int nrow = next * rpt + gid;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int cv = lg + j * a.tpr;
+      const bool on = j < a.nch && cv < nv;
+      if (on) {
+        float xr[VEC][LIN];
+        if constexpr (VEC == 4) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            constexpr int P = Swz<LIN>::P;
+#pragma unroll
+            for (int t = 0; t < LIN; t += P) {
+              const float* p = xs + Swz<LIN>::at(4 * cv + v, t, nv);
+              if constexpr (P == 4) {
+                const float4 f = *reinterpret_cast<const float4*>(p);
+                xr[v][t] = f.x;
+                xr[v][t + 1] = f.y;
+                xr[v][t + 2] = f.z;
+                xr[v][t + 3] = f.w;
+              } else if constexpr (P == 2) {
+                const float2 f = *reinterpret_cast<const float2*>(p);
+                xr[v][t] = f.x;
+                xr[v][t + 1] = f.y;
+              } else {
+                xr[v][t] = *p;
+              }
+            }
+          }
+        } else {
+          // Narrow inputs (channel count not a multiple of 4, raw tensors only) are read directly.
+          const float* p = cv < a.in.split
+                               ? xsrc + static_cast<std::int64_t>(cv) * LIN
+                               : a.in.plain + b * a.in.plain_stride +
+                                     static_cast<std::int64_t>(cv - a.in.split) * LIN;
+#pragma unroll
+          for (int t = 0; t < LIN; ++t) xr[0][t] = p[t];
+        }
+#pragma unroll
+        for (int t = 0; t < LOUT; ++t)
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int jj = src_index<MODE, K, LIN>(t, k);
+            if (jj >= 0) {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) acc[t] = fmaf(w[j][k][v], xr[v][jj], acc[t]);
+            }
+          }
+        if constexpr (RES) {
+#pragma unroll
+          for (int t = 0; t < LOUT; ++t)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+              acc[LOUT + t] = fmaf(w[j][K][v], xr[v][t], acc[LOUT + t]);
+        }
+      }
+      // Refill this chunk's registers with the next tile's weights.
+      if (more && j < a.nch) load_chunk<K, VEC, RES>(a, nrow, cv, cv < nv && nrow < a.oc, w[j]);
+    }
+
+    rs_step<V, 32>(acc, lane);
+    const int off = rs_offset<V>(lane);
+    if (waves == 1) {
+      if (rs_writer<V>(lane) && row < a.oc) {
+        if (!RES || off < LOUT)
+          a.y[b * a.ys + static_cast<std::int64_t>(row) * LOUT + off] = acc[0] + a.bias[row];
+        else
+          a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + off - LOUT] =
+              acc[0] + a.rbias[row];
+      }
+      continue;
+    }
+    // Several wavefronts per row: combine through LDS.  red holds two alternating buffers of
+    // [row group][wavefront in group][V], so one barrier per tile suffices.
+    float* gred = red + parity * (kThreads / kWave) * V + gid * waves * V;
+    parity ^= 1;
+    if (rs_writer<V>(lane)) gred[wig * V + off] = acc[0];
+    lds_barrier();
+    if (lg < V && row < a.oc) {
+      float sum = 0.0f;
+      for (int wv = 0; wv < waves; ++wv) sum += gred[wv * V + lg];
+      if (!RES || lg < LOUT)
+        a.y[b * a.ys + static_cast<std::int64_t>(row) * LOUT + lg] = sum + a.bias[row];
+      else
+        a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + lg - LOUT] = sum + a.rbias[row];
+    }
+  }
+}
+
+inline std::size_t stage_bytes(int ic, int lin, int vec) {
+  return vec == 4 ? static_cast<std::size_t>(ic) * lin * sizeof(float) : 0;
+}
+
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
+hipError_t launch(const Args& a, int batch, hipStream_t s) {
+  const std::size_t smem = stage_bytes(a.ic, LIN, VEC);
+  auto fn = conv_kernel<MODE, K, LIN, VEC, PRO, RES>;
+  if (smem > 48 * 1024) {  // opt in to more than 48 KB of dynamic LDS (up to 160 KB per CU)
+    static bool raised = false;
+    if (!raised) {
+      const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                static_cast<int>(kMaxStageFloats * sizeof(float)));
+      if (st != hipSuccess) return st;
+      raised = true;
+    }
+  }
+  hipLaunchKernelGGL(fn, dim3(a.blocks, batch), dim3(kThreads), smem, s, a);
+  return hipGetLastError();
+}
+
+template <int MODE, int K, int LIN, int VEC>
+hipError_t by_prologue(int pro, bool res, const Args& a, int batch, hipStream_t s) {
+  if constexpr (VEC == 1) {
+    if (pro == kProPlain && MODE == kConvSame)
+      return res ? launch<MODE, K, LIN, 1, kProPlain, true>(a, batch, s)
+                 : launch<MODE, K, LIN, 1, kProPlain, false>(a, batch, s);
+  } else if constexpr (MODE == kConvSame) {
+    switch (pro) {
+      case kProPlain:
+        return res ? launch<MODE, K, LIN, 4, kProPlain, true>(a, batch, s)
+                   : launch<MODE, K, LIN, 4, kProPlain, false>(a, batch, s);
+      case kProFilm:
+        if (!res) return launch<MODE, K, LIN, 4, kProFilm, false>(a, batch, s);
+        break;
+      case kProResid:
+        return res ? launch<MODE, K, LIN, 4, kProResid, true>(a, batch, s)
+                   : launch<MODE, K, LIN, 4, kProResid, false>(a, batch, s);
+      default:
+        break;
+    }
+  } else {
+    if (!res && pro == kProPlain) return launch<MODE, K, LIN, 4, kProPlain, false>(a, batch, s);
+    if (!res && pro == kProResid) return launch<MODE, K, LIN, 4, kProResid, false>(a, batch, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int MODE, int K, int VEC>
+hipError_t by_lin(int lin, int pro, bool res, const Args& a, int batch, hipStream_t s) {
+  switch (lin) {
+    case 1:
+      if constexpr (MODE != kConvDown) return by_prologue<MODE, K, 1, VEC>(pro, res, a, batch, s);
+      break;
+    case 2: return by_prologue<MODE, K, 2, VEC>(pro, res, a, batch, s);
+    case 4: return by_prologue<MODE, K, 4, VEC>(pro, res, a, batch, s);
+    case 8: return by_prologue<MODE, K, 8, VEC>(pro, res, a, batch, s);
+    case 16: return by_prologue<MODE, K, 16, VEC>(pro, res, a, batch, s);
+    default: break;
+  }
+  return hipErrorInvalidValue;
+}
+
+// Launchers, one translation unit each (they instantiate the kernel for every length/prologue).
+hipError_t launch_same5(int lin, int vec, int pro, bool res, const Args& a, int batch,
+                        hipStream_t s);
+hipError_t launch_same3(int lin, int vec, int pro, bool res, const Args& a, int batch,
+                        hipStream_t s);
+hipError_t launch_resample(int mode, int lin, int pro, const Args& a, int batch, hipStream_t s);
+
+}  // namespace fe::hip::conv

@@ -1,0 +1,86 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace fe::hip::dev {
+
+constexpr int kBlock = 256;
+constexpr int kWave = 64;
+
+// mish(v) = v * tanh(log1p(e^v)).  With e = e^v, tanh(log(1 + e)) = ((1+e)^2 - 1) / ((1+e)^2 + 1)
+// = n / (n + 2), n = e (e + 2): one exponential, no cancellation for v << 0.  For v > 20 the
+// factor rounds to 1 in fp32.
+__device__ __forceinline__ float mish_f(float v) {
+  if (v > 20.0f) return v;
+  const float e = expf(v);
+  const float n = e * (e + 2.0f);
+  return v * (n / (n + 2.0f));
+}
+
+// Same identity with the hardware exp2 (v_exp_f32) and reciprocal (v_rcp_f32), each about 1 ULP:
+// the prologue form, where every workgroup transforms a whole activation tensor.
+__device__ __forceinline__ float mish_fast(float v) {
+  if (v > 20.0f) return v;
+  const float e = __builtin_amdgcn_exp2f(v * 1.44269504088896341f);
+  const float n = e * (e + 2.0f);
+  return v * n * __builtin_amdgcn_rcpf(n + 2.0f);
+}
+
+__device__ __forceinline__ float bf16_to_f32(unsigned short bits) {
+  return __uint_as_float(static_cast<unsigned>(bits) << 16);
+}
+
+// Wavefront reduce-scatter.  On entry every lane holds N partial sums v[0..N); on exit lane l
+// holds max(N/64, 1) finished sums (over all 64 lanes) of the original indices
+// [rs_offset<N>(l), +max(N/64,1)).  Each halving step exchanges half of the remaining values with
+// the partner lane (l ^ mask); once one value remains, plain butterfly steps finish it.
+template <int N, int MASK>
+__device__ __forceinline__ void rs_step(float* v, int lane) {
+  if constexpr (MASK > 0) {
+    if constexpr (N >= 2) {
+      const bool upper = (lane & MASK) != 0;
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        const float send = upper ? v[i] : v[i + N / 2];
+        const float keep = upper ? v[i + N / 2] : v[i];
+        v[i] = keep + __shfl_xor(send, MASK, kWave);
+      }
+      rs_step<N / 2, MASK / 2>(v, lane);
+    } else {
+      v[0] += __shfl_xor(v[0], MASK, kWave);
+      rs_step<1, MASK / 2>(v, lane);
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ int rs_offset(int lane) {
+  int off = 0, n = N;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    if (n >= 2) {
+      if (lane & m) off += n / 2;
+      n /= 2;
+    }
+  }
+  return off;
+}
+
+// Lanes that hold a distinct result after rs_step (the butterfly bits must be zero).
+template <int N>
+__device__ __forceinline__ bool rs_writer(int lane) {
+  if constexpr (N >= kWave) {
+    return true;
+  } else {
+    return (lane & (kWave / N - 1)) == 0;
+  }
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+}  // namespace fe::hip::dev

@@ -126,8 +126,29 @@ bool supported_shape(const Config& c, std::string& err) {
     return false;
   }
   const std::size_t h = c.horizon;
-  if (h > 32 || (h & (h - 1)) != 0) {
-    err = "Unsupported horizon (powers of two up to 32 are supported)";
+  if (h > 16 || (h & (h - 1)) != 0) {
+    err = "Unsupported horizon (powers of two up to 16 are supported)";
+    return false;
+  }
+  if (c.groups > 32) {
+    err = "Unsupported GroupNorm group count (at most 32)";
+    return false;
+  }
+  for (std::size_t s = 0; s < c.stages; ++s) {
+    if (c.dims[s] % (4 * c.groups) != 0 || c.dims[s] > 4096) {
+      err = "Unsupported U-Net width (each width must be a multiple of 4 * groups, at most 4096)";
+      return false;
+    }
+    // A workgroup stages one sample's activation in LDS: width * length <= 8192 floats per stage
+    // (up-stage inputs, twice that, are the 64 KB maximum).
+    if (c.dims[s] * (h >> s) > 8192) {
+      err = "Unsupported U-Net size (width * length must be at most 8192 at every stage)";
+      return false;
+    }
+  }
+  if (!fe::hip::update_supported(static_cast<int>(c.dims[0]), static_cast<int>(kFinalNormGroups),
+                                 static_cast<int>(c.horizon), static_cast<int>(c.action_dim))) {
+    err = "Unsupported final layer shape";
     return false;
   }
   return true;
@@ -165,13 +186,11 @@ struct Block {
   NormSlot n1, n2;
   bool identity = false;
   std::size_t ic = 0, oc = 0, len = 0;
-  std::size_t film_off = 0;             // row offset of this block's 2*oc FiLM outputs
+  std::size_t film_off = 0;  // row offset of this block's 2*oc FiLM outputs
   const fe::TensorInfo* film_w = nullptr;
   const fe::TensorInfo* film_b = nullptr;
-  std::size_t h1_off = 0, h2_off = 0, r_off = 0;  // activations [B][oc][len]
-  // Output view: base offset and per-sample stride (floats).
-  std::size_t out_off = 0;
-  std::size_t out_stride = 0;
+  std::size_t h1_off = 0, h2_off = 0, r_off = 0;  // raw conv outputs [B][oc][len]
+  std::size_t xmat_off = 0;                       // materialised block input [B][ic][len]
 };
 
 struct GraphEntry {
@@ -221,15 +240,15 @@ struct FeEngine {
   Block mid[2];
   Block up[kMaxStages][2];
   ConvSlot us[kMaxStages];
-  std::size_t concat[kMaxStages] = {};  // up stage u concat buffer [B][2*high][len]
+  std::size_t concat[kMaxStages] = {};  // up stage u input [x ; skip] buffer [B][2*high][len]
   std::size_t fconv_out = 0;
   ConvSlot fconv, fout;
   NormSlot fnorm;
   std::size_t max_nfe = 0;
   std::size_t time_m = 0, film_table = 0, film_cond = 0;
+  std::size_t ddim_table = 0;  // FiLM time rows for every train timestep [T][F] (epsilon models)
   std::size_t x_state = 0, x_in = 0, k_stages = 0;
   std::size_t in_cond = 0, in_noise = 0, out_action = 0, seed_dev = 0;
-  std::size_t up_in[kMaxStages] = {};   // input of up stage u (its concat buffer)
   std::size_t final_in = 0;
 
   std::list<GraphEntry> graphs;  // most recently used first
@@ -399,6 +418,7 @@ struct Builder {
     e.film_wt = plan.take(c.tdim * F * 4);
     e.film_wc = plan.take(c.cond_dim * F * 4);
     e.film_bias = plan.take(F * 4);
+    if (c.prediction == 0) e.ddim_table = plan.take(c.train_timesteps * F * 4);
 
     // Per-call buffers.  U-Net evaluations per call: diffusion <= T steps, flow RK4 4 per step.
     e.max_nfe = std::max<std::size_t>(c.train_timesteps, 1024);
@@ -414,7 +434,8 @@ struct Builder {
     e.out_action = plan.take(B * v * 4);
     e.seed_dev = plan.take(8);
 
-    // Activations.
+    // Activations.  Raw conv outputs per block; the block input is materialised (by the next
+    // op's prologue) only when it is needed again as an identity residual.
     for (std::size_t u = 0; u + 1 < c.stages; ++u) {
       const Block& r0 = e.up[u][0];
       e.concat[u] = plan.take(B * r0.ic * r0.len * 4);
@@ -423,37 +444,15 @@ struct Builder {
       blk.h1_off = plan.take(B * blk.oc * blk.len * 4);
       blk.h2_off = plan.take(B * blk.oc * blk.len * 4);
       if (!blk.identity) blk.r_off = plan.take(B * blk.oc * blk.len * 4);
+      else blk.xmat_off = plan.take(B * blk.ic * blk.len * 4);
     };
     for (std::size_t s = 0; s < c.stages; ++s) {
       for (int k = 0; k < 2; ++k) acts(e.down[s][k]);
-      Block& r0 = e.down[s][0];
-      r0.out_off = plan.take(B * r0.oc * r0.len * 4);
-      r0.out_stride = r0.oc * r0.len;
-      Block& r1 = e.down[s][1];
-      if (s >= 1) {
-        // Skip tensor: second half of the concat buffer of up stage S-1-s.
-        const std::size_t u = c.stages - 1 - s;
-        r1.out_off = e.concat[u] + r1.oc * r1.len * 4;
-        r1.out_stride = 2 * r1.oc * r1.len;
-      } else {
-        r1.out_off = plan.take(B * r1.oc * r1.len * 4);
-        r1.out_stride = r1.oc * r1.len;
-      }
-      if (s + 1 < c.stages) e.ds_out[s] = plan.take(B * r1.oc * (r1.len / 2) * 4);
+      if (s + 1 < c.stages) e.ds_out[s] = plan.take(B * c.dims[s] * (e.down[s][1].len / 2) * 4);
     }
     for (int m = 0; m < 2; ++m) acts(e.mid[m]);
-    e.mid[0].out_off = plan.take(B * bottom * e.mid[0].len * 4);
-    e.mid[0].out_stride = bottom * e.mid[0].len;
-    e.mid[1].out_off = e.concat[0];
-    e.mid[1].out_stride = 2 * bottom * e.mid[1].len;
-    for (std::size_t u = 0; u + 1 < c.stages; ++u) {
-      for (int k = 0; k < 2; ++k) {
-        Block& blk = e.up[u][k];
-        acts(blk);
-        blk.out_off = plan.take(B * blk.oc * blk.len * 4);
-        blk.out_stride = blk.oc * blk.len;
-      }
-    }
+    for (std::size_t u = 0; u + 1 < c.stages; ++u)
+      for (int k = 0; k < 2; ++k) acts(e.up[u][k]);
     e.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
     e.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
     return true;
@@ -616,130 +615,256 @@ void bind_all(FeEngine& e) {
     if (fe_st_ != hipSuccess) return fe_st_; \
   } while (0)
 
-hipError_t enqueue_block(FeEngine& e, const Block& b, const float* x, std::int64_t xs, int batch,
-                         const float* film_row) {
+// How the current activation tensor is read: a plain tensor, or "virtual" as
+// Y = mish(GroupNorm(src)) + res (a ResidualBlock output that is never stored whole).
+struct Act {
+  bool virt = false;
+  const float* p = nullptr;  // plain tensor, or the raw source of a virtual one
+  std::int64_t stride = 0;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  const float* res = nullptr;
+  std::int64_t res_stride = 0;
+  int channels = 0;
+};
+
+fe::hip::ConvInput input_of(const FeEngine& e, const Act& in, float* mat, std::int64_t mat_stride) {
+  fe::hip::ConvInput ci;
+  ci.src = in.p;
+  ci.src_stride = in.stride;
+  ci.split = in.channels;
+  if (in.virt) {
+    ci.norm = true;
+    ci.gamma = in.gamma;
+    ci.beta = in.beta;
+    ci.groups = static_cast<int>(e.cfg.groups);
+    ci.res = in.res;
+    ci.res_stride = in.res_stride;
+    ci.mat = mat;
+    ci.mat_stride = mat_stride;
+  }
+  return ci;
+}
+
+// One ResidualBlock (diffusion.cc:724-773) as two fused launches:
+//   K1: [conv1 | res 1x1](prologue(input))      -> h1, r
+//   K2: conv2(FiLM(mish(GN1(h1))))               -> h2
+// and returns its output as the virtual Y = mish(GN2(h2)) + (identity ? input : r).
+hipError_t enqueue_block(FeEngine& e, const Block& b, const Act& in, int batch,
+                         const float* film_row, float* skip_mat, std::int64_t skip_stride,
+                         Act& out) {
   using namespace fe::hip;
   hipStream_t s = e.stream;
   const std::int64_t act = static_cast<std::int64_t>(b.oc * b.len);
   float* h1 = e.ptr(b.h1_off);
   float* h2 = e.ptr(b.h2_off);
-  FE_TRY(conv(b.c1.op, x, xs, View{h1, act}, batch, s));
-  const float* res = x;
-  std::int64_t res_stride = xs;
-  if (!b.identity) {
-    float* r = e.ptr(b.r_off);
-    FE_TRY(conv(b.res.op, x, xs, View{r, act}, batch, s));
-    res = r;
-    res_stride = act;
+  // Where the (virtual) input is materialised, when something reads it again.
+  float* mat = nullptr;
+  std::int64_t mat_stride = 0;
+  if (in.virt) {
+    if (skip_mat) {
+      mat = skip_mat;
+      mat_stride = skip_stride;
+    } else if (b.identity) {
+      mat = e.ptr(b.xmat_off);
+      mat_stride = static_cast<std::int64_t>(b.ic * b.len);
+    }
   }
-  NormActOp n1{};
-  n1.gamma = e.ptr(b.n1.g_off);
-  n1.beta = e.ptr(b.n1.b_off);
-  n1.c = static_cast<int>(b.oc);
-  n1.len = static_cast<int>(b.len);
-  n1.groups = static_cast<int>(e.cfg.groups);
-  n1.film_time = film_row;
-  n1.film_cond = e.ptr(e.film_cond);
-  n1.film_cond_stride = static_cast<std::int64_t>(e.film_total);
-  n1.film_off = static_cast<int>(b.film_off);
-  FE_TRY(norm_act(n1, h1, act, View{h1, act}, batch, s));
-  FE_TRY(conv(b.c2.op, h1, act, View{h2, act}, batch, s));
-  NormActOp n2{};
-  n2.gamma = e.ptr(b.n2.g_off);
-  n2.beta = e.ptr(b.n2.b_off);
-  n2.c = static_cast<int>(b.oc);
-  n2.len = static_cast<int>(b.len);
-  n2.groups = static_cast<int>(e.cfg.groups);
-  n2.res = res;
-  n2.res_stride = res_stride;
-  return norm_act(n2, h2, act, View{e.ptr(b.out_off), static_cast<std::int64_t>(b.out_stride)},
-                  batch, s);
+  ConvInput ci = input_of(e, in, mat, mat_stride);
+  float* r = b.identity ? nullptr : e.ptr(b.r_off);
+  FE_TRY(conv_fused(b.c1.op, b.identity ? nullptr : &b.res.op, ci, View{h1, act}, View{r, act},
+                    batch, s));
+  ConvInput c2{};
+  c2.src = h1;
+  c2.src_stride = act;
+  c2.split = static_cast<int>(b.oc);
+  c2.norm = true;
+  c2.gamma = e.ptr(b.n1.g_off);
+  c2.beta = e.ptr(b.n1.b_off);
+  c2.groups = static_cast<int>(e.cfg.groups);
+  c2.film_time = film_row;
+  c2.film_cond = e.ptr(e.film_cond);
+  c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
+  c2.film_off = static_cast<int>(b.film_off);
+  FE_TRY(conv_fused(b.c2.op, nullptr, c2, View{h2, act}, View{}, batch, s));
+  out = Act{};
+  out.virt = true;
+  out.p = h2;
+  out.stride = act;
+  out.gamma = e.ptr(b.n2.g_off);
+  out.beta = e.ptr(b.n2.b_off);
+  out.channels = static_cast<int>(b.oc);
+  if (b.identity) {
+    out.res = in.virt ? mat : in.p;
+    out.res_stride = in.virt ? mat_stride : in.stride;
+  } else {
+    out.res = r;
+    out.res_stride = act;
+  }
+  return hipSuccess;
 }
 
-// One U-Net evaluation on xin (FiLM time row `film_row`), ending with `upd`.
+// One U-Net evaluation on xin (FiLM time row `film_row`), ending with `upd`
+// (diffusion.cc:793-914).
 hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::UpdateOp upd) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   hipStream_t s = e.stream;
-  const float* x = e.ptr(e.x_in);
-  std::int64_t xs = static_cast<std::int64_t>(c.action_dim * c.horizon);
+  Act x;
+  x.p = e.ptr(e.x_in);
+  x.stride = static_cast<std::int64_t>(c.action_dim * c.horizon);
+  x.channels = static_cast<int>(c.action_dim);
+  Act y;
   for (std::size_t st = 0; st < c.stages; ++st) {
-    for (int k = 0; k < 2; ++k) {
-      const Block& b = e.down[st][k];
-      FE_TRY(enqueue_block(e, b, x, xs, batch, film_row));
-      x = e.ptr(b.out_off);
-      xs = static_cast<std::int64_t>(b.out_stride);
-    }
+    FE_TRY(enqueue_block(e, e.down[st][0], x, batch, film_row, nullptr, 0, y));
+    x = y;
+    FE_TRY(enqueue_block(e, e.down[st][1], x, batch, film_row, nullptr, 0, y));
+    x = y;
     if (st + 1 < c.stages) {
+      // Downsample1d; its prologue materialises the stage output as the skip tensor of up stage
+      // S-1-st (second half of that stage's input buffer).  Stage 0's skip is never read.
       const ConvSlot& d = e.ds[st];
-      float* y = e.ptr(e.ds_out[st]);
-      const std::int64_t ys = static_cast<std::int64_t>(d.op.oc) * d.op.lout;
-      FE_TRY(conv(d.op, x, xs, View{y, ys}, batch, s));
-      x = y;
-      xs = ys;
+      float* skip = nullptr;
+      std::int64_t skip_stride = 0;
+      if (st >= 1) {
+        const std::size_t u = c.stages - 1 - st;
+        skip = e.ptr(e.concat[u]) + d.op.ic * d.op.lin;
+        skip_stride = static_cast<std::int64_t>(e.up[u][0].ic * e.up[u][0].len);
+      }
+      ConvInput ci = input_of(e, x, skip, skip_stride);
+      float* out = e.ptr(e.ds_out[st]);
+      const std::int64_t os = static_cast<std::int64_t>(d.op.oc) * d.op.lout;
+      FE_TRY(conv_fused(d.op, nullptr, ci, View{out, os}, View{}, batch, s));
+      x = Act{};
+      x.p = out;
+      x.stride = os;
+      x.channels = d.op.oc;
     }
   }
-  for (int m = 0; m < 2; ++m) {
-    const Block& b = e.mid[m];
-    FE_TRY(enqueue_block(e, b, x, xs, batch, film_row));
-    x = e.ptr(b.out_off);
-    xs = static_cast<std::int64_t>(b.out_stride);
+  // Mid blocks; the first one's prologue materialises the bottom stage output as the skip tensor
+  // of up stage 0.
+  {
+    const Block& m0 = e.mid[0];
+    float* skip = e.ptr(e.concat[0]) + m0.ic * m0.len;
+    const std::int64_t skip_stride = static_cast<std::int64_t>(e.up[0][0].ic * e.up[0][0].len);
+    FE_TRY(enqueue_block(e, m0, x, batch, film_row, skip, skip_stride, y));
+    x = y;
+    FE_TRY(enqueue_block(e, e.mid[1], x, batch, film_row, nullptr, 0, y));
+    x = y;
   }
   for (std::size_t u = 0; u + 1 < c.stages; ++u) {
-    // Input of up stage u is its concat buffer [x ; skip].
-    x = e.ptr(e.concat[u]);
-    xs = static_cast<std::int64_t>(e.up[u][0].ic * e.up[u][0].len);
-    for (int k = 0; k < 2; ++k) {
-      const Block& b = e.up[u][k];
-      FE_TRY(enqueue_block(e, b, x, xs, batch, film_row));
-      x = e.ptr(b.out_off);
-      xs = static_cast<std::int64_t>(b.out_stride);
-    }
-    const ConvSlot& up = e.us[u];
-    View y;
-    if (u + 2 < c.stages) {
-      y.p = e.ptr(e.concat[u + 1]);
-      y.stride = static_cast<std::int64_t>(e.up[u + 1][0].ic * e.up[u + 1][0].len);
+    const Block& r0 = e.up[u][0];
+    const std::int64_t cs = static_cast<std::int64_t>(r0.ic * r0.len);
+    const int half = static_cast<int>(r0.ic / 2);
+    // Input [x ; skip]: x is the virtual mid output (u == 0) or the previous upsample output that
+    // was written into the first half of this buffer.
+    Act cat;
+    if (u == 0) {
+      cat = x;
     } else {
-      y.p = e.ptr(e.final_in);
-      y.stride = static_cast<std::int64_t>(c.dims[0] * c.horizon);
+      cat.p = e.ptr(e.concat[u]);
+      cat.stride = cs;
+      cat.channels = half;
     }
-    FE_TRY(conv(up.op, x, xs, y, batch, s));
+    // enqueue_block's input descriptor covers channels [0, half); the skip half is plain.
+    Act in = cat;
+    in.channels = half;
+    {
+      using namespace fe::hip;
+      hipStream_t s2 = e.stream;
+      const std::int64_t act = static_cast<std::int64_t>(r0.oc * r0.len);
+      ConvInput ci = input_of(e, in, nullptr, 0);
+      ci.plain = e.ptr(e.concat[u]) + half * r0.len;
+      ci.plain_stride = cs;
+      FE_TRY(conv_fused(r0.c1.op, &r0.res.op, ci, View{e.ptr(r0.h1_off), act},
+                        View{e.ptr(r0.r_off), act}, batch, s2));
+      ConvInput c2{};
+      c2.src = e.ptr(r0.h1_off);
+      c2.src_stride = act;
+      c2.split = static_cast<int>(r0.oc);
+      c2.norm = true;
+      c2.gamma = e.ptr(r0.n1.g_off);
+      c2.beta = e.ptr(r0.n1.b_off);
+      c2.groups = static_cast<int>(c.groups);
+      c2.film_time = film_row;
+      c2.film_cond = e.ptr(e.film_cond);
+      c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
+      c2.film_off = static_cast<int>(r0.film_off);
+      FE_TRY(conv_fused(r0.c2.op, nullptr, c2, View{e.ptr(r0.h2_off), act}, View{}, batch, s2));
+      y = Act{};
+      y.virt = true;
+      y.p = e.ptr(r0.h2_off);
+      y.stride = act;
+      y.gamma = e.ptr(r0.n2.g_off);
+      y.beta = e.ptr(r0.n2.b_off);
+      y.res = e.ptr(r0.r_off);
+      y.res_stride = act;
+      y.channels = static_cast<int>(r0.oc);
+      x = y;
+    }
+    FE_TRY(enqueue_block(e, e.up[u][1], x, batch, film_row, nullptr, 0, y));
+    x = y;
+    // Upsample1d into the first half of the next up stage's input, or the final conv input.
+    const ConvSlot& up = e.us[u];
+    View dst;
+    if (u + 2 < c.stages) {
+      dst.p = e.ptr(e.concat[u + 1]);
+      dst.stride = static_cast<std::int64_t>(e.up[u + 1][0].ic * e.up[u + 1][0].len);
+    } else {
+      dst.p = e.ptr(e.final_in);
+      dst.stride = static_cast<std::int64_t>(c.dims[0] * c.horizon);
+    }
+    ConvInput ci = input_of(e, x, nullptr, 0);
+    FE_TRY(conv_fused(up.op, nullptr, ci, dst, View{}, batch, s));
   }
   const std::int64_t fs = static_cast<std::int64_t>(c.dims[0] * c.horizon);
   float* fo = e.ptr(e.fconv_out);
-  FE_TRY(conv(e.fconv.op, e.ptr(e.final_in), fs, View{fo, fs}, batch, s));
-  NormActOp fn{};
-  fn.gamma = e.ptr(e.fnorm.g_off);
-  fn.beta = e.ptr(e.fnorm.b_off);
-  fn.c = static_cast<int>(c.dims[0]);
-  fn.len = static_cast<int>(c.horizon);
-  fn.groups = static_cast<int>(kFinalNormGroups);
-  FE_TRY(norm_act(fn, fo, fs, View{fo, fs}, batch, s));
+  ConvInput fi{};
+  fi.src = e.ptr(e.final_in);
+  fi.src_stride = fs;
+  fi.split = static_cast<int>(c.dims[0]);
+  FE_TRY(conv_fused(e.fconv.op, nullptr, fi, View{fo, fs}, View{}, batch, s));
   upd.c0 = static_cast<int>(c.dims[0]);
   upd.horizon = static_cast<int>(c.horizon);
   upd.action_dim = static_cast<int>(c.action_dim);
   upd.h = fo;
+  upd.gamma = e.ptr(e.fnorm.g_off);
+  upd.beta = e.ptr(e.fnorm.b_off);
+  upd.groups = static_cast<int>(kFinalNormGroups);
   upd.wo = static_cast<const float*>(e.fout.op.w);
   upd.bo = e.fout.op.b;
   return update(upd, batch, s);
 }
 
 // FiLM tables for `count` U-Net evaluations and the per-sample condition part.
-hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int batch) {
+// FiLM time rows W_t mish(temb_mlp(t_n)) + b for `count` U-Net evaluations into `table`.
+// The time MLP output already carries its Mish (the reference applies Mish to the whole FiLM
+// input [t_emb ; cond] once, diffusion.cc:818-820), so the projection splits exactly into a time
+// part and a condition part.
+hipError_t enqueue_film_time(FeEngine& e, const fe::hip::TimeSpec& ts, int count, float* table) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   const int F = static_cast<int>(e.film_total);
   FE_TRY(time_mlp(ts, count, e.ptr(e.te1w), e.ptr(e.te1b), e.ptr(e.te2w), e.ptr(e.te2b),
                   static_cast<int>(c.tdim), e.ptr(e.time_m), e.stream));
-  // The time MLP output already carries its Mish (the reference applies Mish to the whole FiLM
-  // input [t_emb ; cond] once, diffusion.cc:818-820).
-  FE_TRY(film_gemm(e.ptr(e.time_m), static_cast<std::int64_t>(c.tdim), count,
-                   static_cast<int>(c.tdim), e.ptr(e.film_wt), e.ptr(e.film_bias), F, false,
-                   e.ptr(e.film_table), F, e.stream));
-  return film_gemm(e.ptr(e.in_cond), static_cast<std::int64_t>(c.cond_dim), batch,
-                   static_cast<int>(c.cond_dim), e.ptr(e.film_wc), nullptr, F, true,
-                   e.ptr(e.film_cond), F, e.stream);
+  return film_gemm(e.ptr(e.time_m), static_cast<std::int64_t>(c.tdim), count,
+                   static_cast<int>(c.tdim), e.ptr(e.film_wt), e.ptr(e.film_bias), F, false, table,
+                   F, e.stream);
+}
+
+// Condition part W_c mish(cond_b) for every sample; once per sampling call (the condition is
+// the same for every U-Net evaluation of a call).
+hipError_t enqueue_film_cond(FeEngine& e, int batch) {
+  const Config& c = e.cfg;
+  const int F = static_cast<int>(e.film_total);
+  return fe::hip::film_gemm(e.ptr(e.in_cond), static_cast<std::int64_t>(c.cond_dim), batch,
+                            static_cast<int>(c.cond_dim), e.ptr(e.film_wc), nullptr, F, true,
+                            e.ptr(e.film_cond), F, e.stream);
+}
+
+hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int batch) {
+  FE_TRY(enqueue_film_time(e, ts, count, e.ptr(e.film_table)));
+  return enqueue_film_cond(e, batch);
 }
 
 // Whole DDIM/DDPM sampling call (diffusion.cc:916-1035) for `batch` samples.
@@ -750,11 +875,7 @@ hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int sche
   const std::size_t ratio = c.train_timesteps / steps;
   FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
-  TimeSpec ts;
-  ts.mode = kTimesDiffusion;
-  ts.steps = static_cast<int>(steps);
-  ts.ratio = static_cast<int>(ratio);
-  FE_TRY(enqueue_film(e, ts, static_cast<int>(steps), batch));
+  FE_TRY(enqueue_film_cond(e, batch));
   std::uint64_t noisy_steps = 0;
   for (std::size_t i = 0; i < steps; ++i) {
     const std::size_t t = (steps - 1 - i) * ratio;
@@ -786,7 +907,7 @@ hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int sche
       u.noise_offset = noisy_steps * e.values;
       if (prev >= 0) ++noisy_steps;
     }
-    const float* row = e.ptr(e.film_table) + i * e.film_total;
+    const float* row = e.ptr(e.ddim_table) + t * e.film_total;
     FE_TRY(enqueue_unet(e, batch, row, u));
   }
   return finish_sample(e.ptr(e.x_state), e.ptr(e.amin), e.ptr(e.amax), e.ptr(e.out_action), batch,
@@ -1068,6 +1189,17 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   if ((st = upload_weights(*e, *ck)) != hipSuccess) {
     hip_fail("Weight upload failed", st);
     return nullptr;
+  }
+  if (e->cfg.prediction == 0) {
+    // FiLM time rows for every train timestep, computed once on the device.
+    fe::hip::TimeSpec ts;
+    ts.mode = fe::hip::kTimesIndex;
+    if ((st = enqueue_film_time(*e, ts, static_cast<int>(e->cfg.train_timesteps),
+                                e->ptr(e->ddim_table))) != hipSuccess ||
+        (st = hipStreamSynchronize(e->stream)) != hipSuccess) {
+      hip_fail("FiLM time table failed", st);
+      return nullptr;
+    }
   }
   return e.release();
 }

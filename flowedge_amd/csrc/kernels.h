@@ -38,34 +38,50 @@ struct View {
   std::int64_t stride = 0;  // floats between samples
 };
 
-// y = conv(x) + bias for `batch` samples.
-hipError_t conv(const ConvOp& op, const float* x, std::int64_t x_stride, View y, int batch,
-                hipStream_t stream);
-
-// GroupNorm affine, Mish, optional FiLM (scale * v + shift) and optional residual add:
-//   v = mish(gn(x));  v = scale[c] * v + shift[c];  v += res
-// FiLM values are time[off + c] + cond[b][off + c] (scale) and time[off + C + c] +
-// cond[b][off + C + c] (shift).
-struct NormActOp {
+// Input of a fused convolution.  Channels [0, split) come from `src` (a raw producer output,
+// bias included) through the optional prologue
+//     v = mish(GroupNorm(src))           (statistics over all `split` channels of the sample)
+//     v = scale[c] * v + shift[c]        (FiLM, when film_time != null)
+//     v += res[c]                        (residual, when res != null)
+// and are written to `mat` (when non-null) so later ops can read them as a plain tensor;
+// channels [split, ic) are read unchanged from `plain`.  Without `norm`, src channels are read
+// unchanged too.
+struct ConvInput {
+  const float* src = nullptr;
+  std::int64_t src_stride = 0;
+  int split = 0;
+  bool norm = false;
   const float* gamma = nullptr;
   const float* beta = nullptr;
-  int c = 0, len = 0, groups = 0;
-  const float* film_time = nullptr;   // null: no FiLM
+  int groups = 1;
+  const float* film_time = nullptr;
   const float* film_cond = nullptr;
   std::int64_t film_cond_stride = 0;
   int film_off = 0;
-  const float* res = nullptr;         // null: no residual
+  const float* res = nullptr;
   std::int64_t res_stride = 0;
+  float* mat = nullptr;
+  std::int64_t mat_stride = 0;
+  const float* plain = nullptr;
+  std::int64_t plain_stride = 0;
 };
-hipError_t norm_act(const NormActOp& op, const float* x, std::int64_t x_stride, View y, int batch,
-                    hipStream_t stream);
+
+// y = conv(input) + bias, and optionally yr = res1x1(input) + bias from the same prologue (the
+// residual 1x1 projection of a ResidualBlock reads the same input as its first conv).
+hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
+                      View yr, int batch, hipStream_t stream);
+
+// Returns false when conv_fused has no kernel for this shape: `res1x1` with a fused projection,
+// `split` channels from the prologue source, `norm` with a GroupNorm prologue.
+bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm);
 
 // Timestep of the n-th U-Net evaluation of a sampling call, derived on the device:
 //   kTimesSingle: t = t0
 //   kTimesDiffusion: t_n = (steps - 1 - n) * ratio         (diffusion.cc:984-990)
 //   kTimesFlow: step s = n / stages, stage j = n % stages, dt = 1/steps, t = s dt, stage offsets
 //     Euler {0}, Heun {0, dt}, RK4 {0, dt/2, dt/2, dt}   (flow.cc:291-318)
-enum TimesMode : int { kTimesSingle = 0, kTimesDiffusion = 1, kTimesFlow = 2 };
+//   kTimesIndex: t_n = n (the table of every train timestep)
+enum TimesMode : int { kTimesSingle = 0, kTimesDiffusion = 1, kTimesFlow = 2, kTimesIndex = 3 };
 struct TimeSpec {
   int mode = kTimesSingle;
   float t0 = 0.0f;
@@ -87,7 +103,8 @@ hipError_t film_gemm(const float* in, std::int64_t in_stride, int n, int kdim, c
 hipError_t begin_sample(const float* noise, float* x, float* xin, int batch, int horizon,
                         int action_dim, hipStream_t stream);
 
-// Sampler update fused into the final 1x1 conv.  eps[b][a][t] = bo[a] + sum_c wo[a][c] h[b][c][t].
+// Final GroupNorm + Mish + 1x1 conv with the sampler update fused into its epilogue:
+//   eps[b][a][t] = bo[a] + sum_c wo[a][c] mish(gn(h))[b][c][t].
 enum UpdateKind : int {
   kUpdateDenoise = 0,  // out[b][t][a] = eps
   kUpdateDDIM = 1,
@@ -101,7 +118,10 @@ enum UpdateKind : int {
 struct UpdateOp {
   int kind = kUpdateDDIM;
   int c0 = 0, horizon = 0, action_dim = 0;
-  const float* h = nullptr;      // [B][c0][H]
+  const float* h = nullptr;      // [B][c0][H] raw final conv output
+  const float* gamma = nullptr;  // final GroupNorm (8 groups) applied with Mish before the 1x1
+  const float* beta = nullptr;
+  int groups = 8;
   const float* wo = nullptr;     // [A][c0]
   const float* bo = nullptr;     // [A]
   float* x = nullptr;            // sampler state [B][A][H]
@@ -120,6 +140,7 @@ struct UpdateOp {
   float dt = 0;
 };
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
+bool update_supported(int c0, int groups, int horizon, int action_dim);
 
 // action[b][t][a] = (x[b][a][t] + 1) / 2 * (max - min) + min   (or a plain transpose when
 // amin == nullptr).

@@ -1,354 +1,28 @@
-// HIP kernels for the Diffusion Policy U-Net on gfx950 (CDNA4).
+// Small kernels of the Diffusion Policy sampler on gfx950: timestep MLP, FiLM projections, sampler
+// begin/finish, and the final GroupNorm + Mish + 1x1 conv with the DDIM / DDPM / flow-ODE update
+// fused into its epilogue.
 //
-// Batch-1 convolutions are weight-streaming GEMVs: each weight element is read once from HBM and
-// multiplied against the L_out input positions it touches.  Weights are repacked at load to
-// [OC][K][IC] so a 64-lane wavefront reads 64 consecutive 16-byte vectors of one (oc, tap) row;
-// each lane keeps the four input channels it owns resident in registers for all taps and rows,
-// and a wavefront reduce-scatter (halving exchange over lane bits) folds the per-lane partial
-// sums so each lane ends holding a distinct finished output.
-//
-// Reference semantics: conv1d diffusion_ops.cc:82-163, conv_transpose1d :165-268, group_norm
-// :270-350, film :352-377, timestep embedding :379-396, mish kernels_cuda.cu:126-133, DDIM/DDPM
-// diffusion.cc:995-1024, flow updates span_ops.h:27-52, unnormalize diffusion.cc:1027-1033.
-#include "kernels.h"
-
+// Reference semantics: timestep embedding diffusion_ops.cc:379-396, time MLP and FiLM input
+// diffusion.cc:810-820, FiLM modulation :747-752, final conv block :895-913, DDIM/DDPM
+// :995-1024, unnormalize :1027-1033, flow updates span_ops.h:27-52 / flow.cc:291-318.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
+#include "device_common.h"
+#include "kernels.h"
+
 namespace fe::hip {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kWave = 64;
-
-// mish(v) = v * tanh(log1p(e^v)).  With e = e^v, tanh(log(1 + e)) = ((1+e)^2 - 1) / ((1+e)^2 + 1)
-// = n / (n + 2), n = e (e + 2): one exponential, no cancellation for v << 0.  For v > 20 the
-// factor rounds to 1 in fp32.
-__device__ __forceinline__ float mish_f(float v) {
-  if (v > 20.0f) return v;
-  const float e = expf(v);
-  const float n = e * (e + 2.0f);
-  return v * (n / (n + 2.0f));
-}
-
-__device__ __forceinline__ float bf16_to_f32(unsigned short bits) {
-  return __uint_as_float(static_cast<unsigned>(bits) << 16);
-}
+using namespace dev;
 
 // ---------------------------------------------------------------------------------------------
-// Wavefront reduce-scatter.  On entry every lane holds N partial sums v[0..N); on exit lane l
-// holds max(N/64, 1) finished sums (over all 64 lanes) of the original indices
-// [rs_offset<N>(l), +max(N/64,1)).  Each halving step exchanges half of the remaining values
-// with the partner lane (l ^ mask); once one value remains, plain butterfly steps finish it.
-// ---------------------------------------------------------------------------------------------
-template <int N, int MASK>
-__device__ __forceinline__ void rs_step(float* v, int lane) {
-  if constexpr (MASK > 0) {
-    if constexpr (N >= 2) {
-      const bool upper = (lane & MASK) != 0;
-#pragma unroll
-      for (int i = 0; i < N / 2; ++i) {
-        const float send = upper ? v[i] : v[i + N / 2];
-        const float keep = upper ? v[i + N / 2] : v[i];
-        v[i] = keep + __shfl_xor(send, MASK, kWave);
-      }
-      rs_step<N / 2, MASK / 2>(v, lane);
-    } else {
-      v[0] += __shfl_xor(v[0], MASK, kWave);
-      rs_step<1, MASK / 2>(v, lane);
-    }
-  }
-}
-
-template <int N>
-__device__ __forceinline__ int rs_offset(int lane) {
-  int off = 0, n = N;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    if (n >= 2) {
-      if (lane & m) off += n / 2;
-      n /= 2;
-    }
-  }
-  return off;
-}
-
-// Lanes that hold a distinct result after rs_step (the butterfly bits must be zero).
-template <int N>
-__device__ __forceinline__ bool rs_writer(int lane) {
-  if constexpr (N >= kWave) {
-    return true;
-  } else {
-    return (lane & (kWave / N - 1)) == 0;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Convolution (weight-streaming GEMV form).
-// ---------------------------------------------------------------------------------------------
-struct ConvArgs {
-  const void* w;
-  const float* bias;
-  const float* x;
-  float* y;
-  std::int64_t xs, ys;
-  int ic, oc;
-  int tpr;  // lanes per row group: 64, 128 or 256
-};
-
-template <int MODE, int LIN>
-struct ConvShape {
-  static constexpr int lout = MODE == kConvSame ? LIN : (MODE == kConvDown ? LIN / 2 : 2 * LIN);
-};
-
-// Input index read by output t through tap k, or -1 when it falls in the zero padding.
-template <int MODE, int K, int LIN>
-__device__ __forceinline__ constexpr int src_index(int t, int k) {
-  if constexpr (MODE == kConvSame) {
-    const int j = t + k - K / 2;
-    return (j >= 0 && j < LIN) ? j : -1;
-  } else if constexpr (MODE == kConvDown) {
-    const int j = 2 * t + k - 1;
-    return (j >= 0 && j < LIN) ? j : -1;
-  } else {
-    // ConvTranspose: output ot = 2 * it + k - 1.
-    const int num = t + 1 - k;
-    if (num < 0 || (num & 1)) return -1;
-    const int j = num / 2;
-    return j < LIN ? j : -1;
-  }
-}
-
-template <int VEC, bool BF16>
-__device__ __forceinline__ void load_w(const void* base, std::int64_t idx, float* out) {
-  if constexpr (BF16) {
-    const unsigned short* p = static_cast<const unsigned short*>(base) + idx;
-    if constexpr (VEC == 4) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(p);
-      out[0] = __uint_as_float(raw.x << 16);
-      out[1] = __uint_as_float(raw.x & 0xffff0000u);
-      out[2] = __uint_as_float(raw.y << 16);
-      out[3] = __uint_as_float(raw.y & 0xffff0000u);
-    } else {
-      out[0] = bf16_to_f32(*p);
-    }
-  } else {
-    const float* p = static_cast<const float*>(base) + idx;
-    if constexpr (VEC == 4) {
-      const float4 v = *reinterpret_cast<const float4*>(p);
-      out[0] = v.x;
-      out[1] = v.y;
-      out[2] = v.z;
-      out[3] = v.w;
-    } else {
-      out[0] = *p;
-    }
-  }
-}
-
-template <int MODE, int K, int LIN, int VEC, int R, bool BF16>
-__global__ __launch_bounds__(kBlock) void conv_kernel(ConvArgs a) {
-  constexpr int LOUT = ConvShape<MODE, LIN>::lout;
-  constexpr int V = R * LOUT;
-  __shared__ float red[4 * V];
-
-  const int tid = threadIdx.x;
-  const int groups = kBlock / a.tpr;
-  const int gid = tid / a.tpr;
-  const int lg = tid - gid * a.tpr;
-  const int row0 = (blockIdx.x * groups + gid) * R;
-  const int b = blockIdx.y;
-  const float* x = a.x + b * a.xs;
-  const int nv = a.ic / VEC;
-
-  float acc[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-
-  for (int cv = lg; cv < nv; cv += a.tpr) {
-    float xr[VEC][LIN];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const float* row = x + static_cast<std::int64_t>(cv * VEC + v) * LIN;
-      if constexpr (LIN % 4 == 0) {
-#pragma unroll
-        for (int j = 0; j < LIN; j += 4) {
-          const float4 q = *reinterpret_cast<const float4*>(row + j);
-          xr[v][j] = q.x;
-          xr[v][j + 1] = q.y;
-          xr[v][j + 2] = q.z;
-          xr[v][j + 3] = q.w;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < LIN; ++j) xr[v][j] = row[j];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int oc = row0 + r;
-      if (oc < a.oc) {
-        float wv[K][VEC];
-#pragma unroll
-        for (int k = 0; k < K; ++k)
-          load_w<VEC, BF16>(a.w, (static_cast<std::int64_t>(oc) * K + k) * a.ic + cv * VEC,
-                            wv[k]);
-#pragma unroll
-        for (int t = 0; t < LOUT; ++t) {
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const int j = src_index<MODE, K, LIN>(t, k);
-            if (j >= 0) {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[r * LOUT + t] = fmaf(wv[k][v], xr[v][j], acc[r * LOUT + t]);
-            }
-          }
-        }
-      }
-    }
-  }
-
-  const int lane = tid & (kWave - 1);
-  rs_step<V, 32>(acc, lane);
-  constexpr int NF = V >= kWave ? V / kWave : 1;
-  const int off = rs_offset<V>(lane);
-  const int waves = a.tpr / kWave;
-  const int wig = lg / kWave;  // wave index inside the row group
-  if (waves == 1) {
-    if (rs_writer<V>(lane)) {
-#pragma unroll
-      for (int i = 0; i < NF; ++i) {
-        const int idx = off + i;
-        const int oc = row0 + idx / LOUT;
-        if (oc < a.oc)
-          a.y[b * a.ys + static_cast<std::int64_t>(oc) * LOUT + (idx % LOUT)] = acc[i] + a.bias[oc];
-      }
-    }
-    return;
-  }
-  // Several waves per row group: combine through LDS.  red holds [wave-in-group][V] for each
-  // group; a block has at most 4 waves in total, so 4 * V floats suffice.
-  float* gred = red + gid * waves * V;
-  if (rs_writer<V>(lane)) {
-#pragma unroll
-    for (int i = 0; i < NF; ++i) gred[wig * V + off + i] = acc[i];
-  }
-  __syncthreads();
-  for (int idx = lg; idx < V; idx += a.tpr) {
-    float s = 0.0f;
-    for (int w = 0; w < waves; ++w) s += gred[w * V + idx];
-    const int oc = row0 + idx / LOUT;
-    if (oc < a.oc)
-      a.y[b * a.ys + static_cast<std::int64_t>(oc) * LOUT + (idx % LOUT)] = s + a.bias[oc];
-  }
-}
-
-constexpr int kRows = 2;
-
-template <int MODE, int K, int LIN, int VEC, bool BF16>
-hipError_t launch_conv_t(const ConvArgs& a, int batch, hipStream_t s) {
-  const int groups = kBlock / a.tpr;
-  const int rows_per_block = groups * kRows;
-  const dim3 grid((a.oc + rows_per_block - 1) / rows_per_block, batch);
-  hipLaunchKernelGGL((conv_kernel<MODE, K, LIN, VEC, kRows, BF16>), grid, dim3(kBlock), 0, s, a);
-  return hipGetLastError();
-}
-
-template <int MODE, int K, int VEC, bool BF16>
-hipError_t dispatch_lin(const ConvArgs& a, int lin, int batch, hipStream_t s) {
-  switch (lin) {
-    case 1:
-      if constexpr (MODE != kConvDown) return launch_conv_t<MODE, K, 1, VEC, BF16>(a, batch, s);
-      break;
-    case 2: return launch_conv_t<MODE, K, 2, VEC, BF16>(a, batch, s);
-    case 4: return launch_conv_t<MODE, K, 4, VEC, BF16>(a, batch, s);
-    case 8: return launch_conv_t<MODE, K, 8, VEC, BF16>(a, batch, s);
-    case 16: return launch_conv_t<MODE, K, 16, VEC, BF16>(a, batch, s);
-    case 32:
-      if constexpr (MODE != kConvTranspose) return launch_conv_t<MODE, K, 32, VEC, BF16>(a, batch, s);
-      break;
-    default: break;
-  }
-  return hipErrorInvalidValue;
-}
-
-template <int VEC, bool BF16>
-hipError_t dispatch_mode(const ConvOp& op, const ConvArgs& a, int batch, hipStream_t s) {
-  if (op.mode == kConvSame) {
-    switch (op.k) {
-      case 1: return dispatch_lin<kConvSame, 1, VEC, BF16>(a, op.lin, batch, s);
-      case 3: return dispatch_lin<kConvSame, 3, VEC, BF16>(a, op.lin, batch, s);
-      case 5: return dispatch_lin<kConvSame, 5, VEC, BF16>(a, op.lin, batch, s);
-      default: return hipErrorInvalidValue;
-    }
-  }
-  if (op.mode == kConvDown && op.k == 3) return dispatch_lin<kConvDown, 3, VEC, BF16>(a, op.lin, batch, s);
-  if (op.mode == kConvTranspose && op.k == 4)
-    return dispatch_lin<kConvTranspose, 4, VEC, BF16>(a, op.lin, batch, s);
-  return hipErrorInvalidValue;
-}
-
-// ---------------------------------------------------------------------------------------------
-// GroupNorm + Mish + FiLM + residual.  One block per (group, sample); statistics in fp64 with
-// var = E[x^2] - mean^2 clamped at 0, eps 1e-5 (group_norm, diffusion_ops.cc:270-350).
-// ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ double block_sum(double v, double* sh) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  const int w = threadIdx.x / kWave;
-  __syncthreads();
-  if ((threadIdx.x & (kWave - 1)) == 0) sh[w] = v;
-  __syncthreads();
-  double s = 0.0;
-  for (int i = 0; i < kBlock / kWave; ++i) s += sh[i];
-  return s;
-}
-
-__global__ __launch_bounds__(kBlock) void norm_act_kernel(NormActOp op, const float* x,
-                                                          std::int64_t xs, float* y,
-                                                          std::int64_t ys) {
-  __shared__ double sh[kBlock / kWave];
-  const int g = blockIdx.x, b = blockIdx.y;
-  const int cpg = op.c / op.groups;
-  const int count = cpg * op.len;
-  const std::int64_t base = static_cast<std::int64_t>(g) * count;
-  const float* xb = x + b * xs + base;
-  double sum = 0.0, sq = 0.0;
-  for (int i = threadIdx.x; i < count; i += kBlock) {
-    const double v = static_cast<double>(xb[i]);
-    sum += v;
-    sq += v * v;
-  }
-  sum = block_sum(sum, sh);
-  sq = block_sum(sq, sh);
-  const double mean = sum / static_cast<double>(count);
-  const double var = fmax(0.0, sq / static_cast<double>(count) - mean * mean);
-  const float inv = static_cast<float>(1.0 / sqrt(var + 1e-5));
-  const float mean_f = static_cast<float>(mean);
-  float* yb = y + b * ys + base;
-  const float* rb = op.res ? op.res + b * op.res_stride + base : nullptr;
-  for (int i = threadIdx.x; i < count; i += kBlock) {
-    const int c = g * cpg + i / op.len;
-    float v = fmaf(xb[i] - mean_f, inv * op.gamma[c], op.beta[c]);
-    v = mish_f(v);
-    if (op.film_time) {
-      const float* fc = op.film_cond + b * op.film_cond_stride + op.film_off;
-      const float* ft = op.film_time + op.film_off;
-      const float scale = ft[c] + fc[c];
-      const float shift = ft[op.c + c] + fc[op.c + c];
-      v = fmaf(scale, v, shift);
-    }
-    if (rb) v += rb[i];
-    yb[i] = v;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Time MLP: m = mish(te2(mish(te1(emb(t)) + b1)) + b2), one block per timestep.
+// Time MLP: m = mish(te2(mish(te1(emb(t)) + b1)) + b2), one block per U-Net evaluation.
 // ---------------------------------------------------------------------------------------------
 __device__ float nfe_time(const TimeSpec& ts, int n) {
   if (ts.mode == kTimesSingle) return ts.t0;
+  if (ts.mode == kTimesIndex) return static_cast<float>(n);
   if (ts.mode == kTimesDiffusion) return static_cast<float>((ts.steps - 1 - n) * ts.ratio);
   const int stages = ts.method == 2 ? 4 : (ts.method == 1 ? 2 : 1);
   const int s = n / stages, j = n % stages;
@@ -364,8 +38,8 @@ __global__ __launch_bounds__(kBlock) void time_mlp_kernel(TimeSpec ts, const flo
                                                           const float* b1, const float* w2,
                                                           const float* b2, int tdim, float* m) {
   extern __shared__ float smem[];
-  float* emb = smem;            // [tdim]
-  float* hid = smem + tdim;     // [4 tdim]
+  float* emb = smem;         // [tdim]
+  float* hid = smem + tdim;  // [4 tdim]
   const float t = nfe_time(ts, blockIdx.x);
   const int half = tdim / 2;
   if (half == 1) {
@@ -399,16 +73,22 @@ __global__ __launch_bounds__(kBlock) void time_mlp_kernel(TimeSpec ts, const flo
   }
 }
 
-// out[n][f] = bias[f] + sum_k wt[k][f] * act(in[n][k]); eight rows of n per block, k in chunks.
+// ---------------------------------------------------------------------------------------------
+// FiLM projection: out[n][f] = bias[f] + sum_k wt[k][f] * act(in[n][k]).  A block covers 64
+// consecutive f (one per lane) and 8 rows of n; its four wavefronts split k and combine in LDS.
+// ---------------------------------------------------------------------------------------------
 constexpr int kFilmRows = 8;
 constexpr int kFilmChunk = 256;
 
 __global__ __launch_bounds__(kBlock) void film_gemm_kernel(const float* in, std::int64_t in_stride,
                                                            int n, int kdim, const float* wt,
-                                                           const float* bias, int fdim, int mish_in,
-                                                           float* out, std::int64_t out_stride) {
+                                                           const float* bias, int fdim,
+                                                           int mish_in, float* out,
+                                                           std::int64_t out_stride) {
   __shared__ float act[kFilmRows][kFilmChunk];
-  const int f = blockIdx.x * kBlock + threadIdx.x;
+  __shared__ float part[kBlock / kWave][kFilmRows][kWave];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int f = blockIdx.x * kWave + lane;
   const int n0 = blockIdx.y * kFilmRows;
   float acc[kFilmRows];
 #pragma unroll
@@ -427,18 +107,24 @@ __global__ __launch_bounds__(kBlock) void film_gemm_kernel(const float* in, std:
     }
     __syncthreads();
     if (f < fdim) {
-      for (int k = 0; k < kc; ++k) {
+      for (int k = wave; k < kc; k += kBlock / kWave) {
         const float w = wt[static_cast<std::int64_t>(k0 + k) * fdim + f];
 #pragma unroll
         for (int r = 0; r < kFilmRows; ++r) acc[r] = fmaf(w, act[r][k], acc[r]);
       }
     }
   }
-  if (f < fdim) {
-    const float bb = bias ? bias[f] : 0.0f;
 #pragma unroll
-    for (int r = 0; r < kFilmRows; ++r)
-      if (n0 + r < n) out[(n0 + r) * out_stride + f] = acc[r] + bb;
+  for (int r = 0; r < kFilmRows; ++r) part[wave][r][lane] = acc[r];
+  __syncthreads();
+  for (int i = threadIdx.x; i < kFilmRows * kWave; i += kBlock) {
+    const int r = i / kWave, l = i % kWave;
+    const int ff = blockIdx.x * kWave + l;
+    if (n0 + r < n && ff < fdim) {
+      float s = 0.0f;
+      for (int w = 0; w < kBlock / kWave; ++w) s += part[w][r][l];
+      out[(n0 + r) * out_stride + ff] = s + (bias ? bias[ff] : 0.0f);
+    }
   }
 }
 
@@ -474,17 +160,105 @@ __device__ __forceinline__ float stream_gaussian(std::uint64_t seed, std::uint64
   return (n & 1) ? radius * sinf(angle) : radius * cosf(angle);
 }
 
+constexpr int kMaxUpdateChannelsPerLane = 4;  // c0 <= 1024
+constexpr int kMaxUpdateGroups = 32;
+constexpr int kMaxActions = 64;
+
+// One block per sample.  Lane l owns channels l, l+256, ...: loads them, the block reduces the
+// GroupNorm statistics, applies GN + Mish, and reduces the 1x1 conv over channels per action
+// channel (wavefront reduce-scatter over the H positions + LDS across wavefronts).  The update then
+// runs on the A*H state values.
+template <int H>
 __global__ __launch_bounds__(kBlock) void update_kernel(UpdateOp op) {
+  __shared__ double ps[kBlock * kMaxUpdateChannelsPerLane];
+  __shared__ double pq[kBlock * kMaxUpdateChannelsPerLane];
+  __shared__ float gmean[kMaxUpdateGroups], ginv[kMaxUpdateGroups];
+  __shared__ float red[kBlock / kWave][H];
+  __shared__ float eps[kMaxActions][H];
   const int b = blockIdx.x;
-  const int H = op.horizon, A = op.action_dim;
+  const int A = op.action_dim, C = op.c0;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
-  const float* hb = op.h + static_cast<std::int64_t>(b) * op.c0 * H;
-  for (int i = threadIdx.x; i < A * H; i += kBlock) {
+  const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
+
+  float hv[kMaxUpdateChannelsPerLane][H];
+#pragma unroll
+  for (int i = 0; i < kMaxUpdateChannelsPerLane; ++i) {
+    const int c = tid + i * kBlock;
+    double s = 0.0, q = 0.0;
+#pragma unroll
+    for (int t = 0; t < H; ++t) {
+      hv[i][t] = c < C ? hb[static_cast<std::int64_t>(c) * H + t] : 0.0f;
+      const double d = static_cast<double>(hv[i][t]);
+      s += d;
+      q += d * d;
+    }
+    if (c < C) {
+      ps[c] = s;
+      pq[c] = q;
+    }
+  }
+  __syncthreads();
+  const int cpg = C / op.groups;
+  for (int g = wave; g < op.groups; g += kBlock / kWave) {
+    double s = 0.0, q = 0.0;
+    for (int i = lane; i < cpg; i += kWave) {
+      s += ps[g * cpg + i];
+      q += pq[g * cpg + i];
+    }
+    s = wave_sum(s);
+    q = wave_sum(q);
+    if (lane == 0) {
+      const double n = static_cast<double>(cpg) * H;
+      const double mean = s / n;
+      const double var = fmax(0.0, q / n - mean * mean);
+      gmean[g] = static_cast<float>(mean);
+      ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kMaxUpdateChannelsPerLane; ++i) {
+    const int c = tid + i * kBlock;
+    if (c < C) {
+      const int g = c / cpg;
+      const float scale = ginv[g] * op.gamma[c];
+#pragma unroll
+      for (int t = 0; t < H; ++t) hv[i][t] = mish_f(fmaf(hv[i][t] - gmean[g], scale, op.beta[c]));
+    }
+  }
+  for (int a = 0; a < A; ++a) {
+    float p[H];
+#pragma unroll
+    for (int t = 0; t < H; ++t) p[t] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxUpdateChannelsPerLane; ++i) {
+      const int c = tid + i * kBlock;
+      if (c < C) {
+        const float w = op.wo[static_cast<std::int64_t>(a) * C + c];
+#pragma unroll
+        for (int t = 0; t < H; ++t) p[t] = fmaf(w, hv[i][t], p[t]);
+      }
+    }
+    rs_step<H, 32>(p, lane);
+    constexpr int NF = H >= kWave ? H / kWave : 1;
+    const int off = rs_offset<H>(lane);
+    if (rs_writer<H>(lane)) {
+#pragma unroll
+      for (int i = 0; i < NF; ++i) red[wave][off + i] = p[i];
+    }
+    __syncthreads();
+    if (tid < H) {
+      float s = 0.0f;
+      for (int w = 0; w < kBlock / kWave; ++w) s += red[w][tid];
+      eps[a][tid] = s + op.bo[a];
+    }
+    __syncthreads();
+  }
+
+  for (int i = tid; i < A * H; i += kBlock) {
     const int a = i / H, t = i % H;  // state layout [A][H]
-    const float* wr = op.wo + static_cast<std::int64_t>(a) * op.c0;
-    float e = 0.0f;
-    for (int c = 0; c < op.c0; ++c) e = fmaf(wr[c], hb[c * H + t], e);
-    e += op.bo[a];
+    const float e = eps[a][t];
     const std::int64_t si = sample + i;
     switch (op.kind) {
       case kUpdateDenoise:
@@ -555,33 +329,6 @@ __global__ void finish_kernel(const float* x, const float* amin, const float* am
 
 }  // namespace
 
-hipError_t conv(const ConvOp& op, const float* x, std::int64_t x_stride, View y, int batch,
-                hipStream_t stream) {
-  ConvArgs a{};
-  a.w = op.w;
-  a.bias = op.b;
-  a.x = x;
-  a.y = y.p;
-  a.xs = x_stride;
-  a.ys = y.stride;
-  a.ic = op.ic;
-  a.oc = op.oc;
-  const bool vec4 = op.ic % 4 == 0;
-  const int nv = vec4 ? op.ic / 4 : op.ic;
-  a.tpr = nv >= 256 ? 256 : (nv >= 128 ? 128 : 64);
-  if (vec4) return op.bf16 ? dispatch_mode<4, true>(op, a, batch, stream)
-                           : dispatch_mode<4, false>(op, a, batch, stream);
-  return op.bf16 ? dispatch_mode<1, true>(op, a, batch, stream)
-                 : dispatch_mode<1, false>(op, a, batch, stream);
-}
-
-hipError_t norm_act(const NormActOp& op, const float* x, std::int64_t x_stride, View y, int batch,
-                    hipStream_t stream) {
-  hipLaunchKernelGGL(norm_act_kernel, dim3(op.groups, batch), dim3(kBlock), 0, stream, op, x,
-                     x_stride, y.p, y.stride);
-  return hipGetLastError();
-}
-
 hipError_t time_mlp(const TimeSpec& times, int count, const float* w1, const float* b1,
                     const float* w2, const float* b2, int tdim, float* m, hipStream_t stream) {
   const size_t smem = static_cast<size_t>(5 * tdim) * sizeof(float);
@@ -593,7 +340,7 @@ hipError_t time_mlp(const TimeSpec& times, int count, const float* w1, const flo
 hipError_t film_gemm(const float* in, std::int64_t in_stride, int n, int kdim, const float* wt,
                      const float* bias, int fdim, bool mish_in, float* out,
                      std::int64_t out_stride, hipStream_t stream) {
-  const dim3 grid((fdim + kBlock - 1) / kBlock, (n + kFilmRows - 1) / kFilmRows);
+  const dim3 grid((fdim + kWave - 1) / kWave, (n + kFilmRows - 1) / kFilmRows);
   hipLaunchKernelGGL(film_gemm_kernel, grid, dim3(kBlock), 0, stream, in, in_stride, n, kdim, wt,
                      bias, fdim, mish_in ? 1 : 0, out, out_stride);
   return hipGetLastError();
@@ -606,8 +353,22 @@ hipError_t begin_sample(const float* noise, float* x, float* xin, int batch, int
   return hipGetLastError();
 }
 
+bool update_supported(int c0, int groups, int horizon, int action_dim) {
+  return c0 > 0 && c0 <= kBlock * kMaxUpdateChannelsPerLane && groups > 0 &&
+         groups <= kMaxUpdateGroups && c0 % groups == 0 && action_dim > 0 &&
+         action_dim <= kMaxActions &&
+         (horizon == 1 || horizon == 2 || horizon == 4 || horizon == 8 || horizon == 16);
+}
+
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL(update_kernel, dim3(batch), dim3(kBlock), 0, stream, op);
+  if (!update_supported(op.c0, op.groups, op.horizon, op.action_dim)) return hipErrorInvalidValue;
+  switch (op.horizon) {
+    case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(kBlock), 0, stream, op); break;
+    case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(kBlock), 0, stream, op); break;
+    case 4: hipLaunchKernelGGL(update_kernel<4>, dim3(batch), dim3(kBlock), 0, stream, op); break;
+    case 8: hipLaunchKernelGGL(update_kernel<8>, dim3(batch), dim3(kBlock), 0, stream, op); break;
+    default: hipLaunchKernelGGL(update_kernel<16>, dim3(batch), dim3(kBlock), 0, stream, op); break;
+  }
   return hipGetLastError();
 }
 
