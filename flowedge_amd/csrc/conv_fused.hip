@@ -96,7 +96,15 @@ hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& i
   if (res && (res1x1->k != 1 || res1x1->ic != op.ic || res1x1->oc != op.oc || yr.p == nullptr))
     return hipErrorInvalidValue;
   if (batch <= 0 || batch > 65535) return hipErrorInvalidValue;
+  // Weight tensors are addressed with 32-bit buffer offsets (out-of-range marker at 2 GiB).
+  const std::uint64_t wbytes = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
+  const std::uint64_t rwbytes =
+      res ? static_cast<std::uint64_t>(op.oc) * op.ic * (res1x1->bf16 ? 2 : 4) : 0;
+  if (wbytes >= kOutOfRange || rwbytes >= kOutOfRange) return hipErrorInvalidValue;
+  if (res && p.vec == 4 && res1x1->bf16 != op.bf16) return hipErrorInvalidValue;
   Args a{};
+  a.wbytes = static_cast<unsigned>(wbytes);
+  a.rwbytes = static_cast<unsigned>(rwbytes);
   a.w = op.w;
   a.bias = op.b;
   a.y = y.p;

@@ -10,7 +10,7 @@
 // VGPRs per lane hold the weights in flight).  A workgroup
 //   1. requests its share of the input (raw producer output, residual, GroupNorm/FiLM parameters)
 //      into registers,
-//   2. then requests every weight vector of its first row tile (up to 160 floats per lane), so the
+//   2. then requests every weight vector of its first row tile (up to 128 floats per lane), so the
 //      input arrives first and the weights keep streaming during the prologue,
 //   3. computes the GroupNorm statistics of the sample (fp64 partials, var = E[x^2] - mean^2 as
 //      group_norm, diffusion_ops.cc:270-350), applies GN + Mish (+ FiLM) (+ residual), writes its
@@ -40,7 +40,7 @@ constexpr int kThreads = 512;
 constexpr int kMaxStageFloats = 16384;  // staged input per sample: channels * positions (64 KB)
 constexpr int kMaxNormFloats = 8192;    // of which normalised (GroupNorm prologue)
 constexpr int kMaxGroups = 32;
-constexpr int kWeightRegs = 160;        // weight floats in flight per lane
+constexpr int kWeightRegs = 128;        // weight floats in flight per lane
 constexpr int kMaxBlocks = 256;         // one workgroup per CU
 
 // Input prologue kinds (the only ones the U-Net produces).
@@ -59,11 +59,17 @@ __host__ __device__ constexpr int lout_of(int mode, int lin) {
 // at 64 lanes per row, and by 8.
 __host__ __device__ constexpr int chunk_budget(int k, int lin, bool res, int vec) {
   const int taps = k + (res ? 1 : 0);
-  const int regs = lin >= 8 ? kWeightRegs - 32 : kWeightRegs;
+  const int regs = lin >= 16 ? kWeightRegs - 64 : (lin >= 8 ? kWeightRegs - 32 : kWeightRegs);
   const int by_regs = regs / (taps * vec);
   const int by_size = (kMaxStageFloats / (lin * vec) + 63) / 64;
   const int n = by_regs < by_size ? by_regs : by_size;
   return n < 8 ? n : 8;
+}
+
+// Weight floats per lane requested before the input prologue.
+constexpr int kEarlyFloats = 48;
+__host__ __device__ constexpr int early_chunks(int taps) {
+  return kEarlyFloats / (taps * 4) > 0 ? kEarlyFloats / (taps * 4) : 1;
 }
 
 struct Args {
@@ -76,6 +82,7 @@ struct Args {
   float* yr;
   std::int64_t yrs;
   int bf16, rbf16;
+  unsigned wbytes, rwbytes;  // weight tensor sizes (buffer range; < 2 GiB)
   int oc, ic;
   int tiles;   // row tiles of kThreads / tpr rows
   int blocks;  // workgroups (grid.x); workgroup g takes tiles g, g + blocks, ...
@@ -132,21 +139,64 @@ __device__ __forceinline__ void load_w(const void* base, int bf16, std::int64_t 
   }
 }
 
+// Weight vectors are read with buffer loads: an inactive lane or chunk gets an out-of-range offset,
+// which returns zeros without touching memory, so every load is issued unconditionally (no
+// branches around them, and the waits the compiler places for the prologue's reads leave the
+// weight loads in flight).
+constexpr unsigned kOutOfRange = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, kRsrcWord3);
+}
+
+// voff: byte offset of the row/chunk (or kOutOfRange); soff: wave-uniform byte offset of the tap.
+template <bool BF16>
+__device__ __forceinline__ void load_vec4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff,
+                                          float* out) {
+  if constexpr (BF16) {
+    const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    const uint2 raw = __builtin_bit_cast(uint2, t);
+    out[0] = __uint_as_float(raw.x << 16);
+    out[1] = __uint_as_float(raw.x & 0xffff0000u);
+    out[2] = __uint_as_float(raw.y << 16);
+    out[3] = __uint_as_float(raw.y & 0xffff0000u);
+  } else {
+    const auto t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const float4 v = __builtin_bit_cast(float4, t);
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
+    out[3] = v.w;
+  }
+}
+
 // Weights of one input chunk (all taps, then the projection tap) of one row.
-template <int K, int VEC, bool RES>
-__device__ __forceinline__ void load_chunk(const Args& a, int row, int cv, bool valid,
+template <int K, int VEC, bool RES, bool BF16>
+__device__ __forceinline__ void load_chunk(const Args& a, __amdgpu_buffer_rsrc_t wr,
+                                           __amdgpu_buffer_rsrc_t rr, int row, int cv, bool valid,
                                            float (&w)[K + (RES ? 1 : 0)][VEC]) {
-  if (valid) {
+  if constexpr (VEC == 4) {
+    constexpr unsigned es = BF16 ? 2u : 4u;
+    const unsigned voff = valid ? static_cast<unsigned>(row * K * a.ic + cv * 4) * es : kOutOfRange;
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      load_w<VEC>(a.w, a.bf16, (static_cast<std::int64_t>(row) * K + k) * a.ic + cv * VEC, w[k]);
-    if constexpr (RES)
-      load_w<VEC>(a.rw, a.rbf16, static_cast<std::int64_t>(row) * a.ic + cv * VEC, w[K]);
+      load_vec4<BF16>(wr, voff, static_cast<unsigned>(k * a.ic) * es, w[k]);
+    if constexpr (RES) {
+      const unsigned roff = valid ? static_cast<unsigned>(row * a.ic + cv * 4) * es : kOutOfRange;
+      load_vec4<BF16>(rr, roff, 0u, w[K]);
+    }
   } else {
+    // Narrow inputs (first convolution only): plain loads, bf16 decided at run time.
+    if (valid) {
 #pragma unroll
-    for (int k = 0; k < K + (RES ? 1 : 0); ++k)
+      for (int k = 0; k < K; ++k)
+        load_w<1>(a.w, a.bf16, (static_cast<std::int64_t>(row) * K + k) * a.ic + cv, w[k]);
+      if constexpr (RES) load_w<1>(a.rw, a.rbf16, static_cast<std::int64_t>(row) * a.ic + cv, w[K]);
+    } else {
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) w[k][v] = 0.0f;
+      for (int k = 0; k < K + (RES ? 1 : 0); ++k) w[k][0] = 0.0f;
+    }
   }
 }
 
@@ -330,17 +380,13 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
   lds_barrier();
 }
 
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
-__global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool BF16>
+__device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean, float* ginv,
+                                          float* red) {
   constexpr int LOUT = lout_of(MODE, LIN);
   constexpr int TAPS = K + (RES ? 1 : 0);
   constexpr int NCH = chunk_budget(K, LIN, RES, VEC);
   constexpr int V = RES ? 2 * LOUT : LOUT;
-  static_assert(V <= kWave, "one reduced value per lane");
-  extern __shared__ float4 xs4[];
-  float* xs = reinterpret_cast<float*>(xs4);
-  __shared__ float gmean[kMaxGroups], ginv[kMaxGroups];
-  __shared__ float red[2 * (kThreads / kWave) * V];
   const int tid = threadIdx.x;
   const int wg = blockIdx.x;
   const int b = blockIdx.y;
@@ -350,21 +396,36 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
   const int nv = a.ic / VEC;
   const int lane = tid & (kWave - 1);
 
+  const __amdgpu_buffer_rsrc_t wr = buffer_of(a.w, a.wbytes);
+  const __amdgpu_buffer_rsrc_t rr = buffer_of(RES ? a.rw : a.w, RES ? a.rwbytes : a.wbytes);
   StageRegs<LIN, PRO> st;
-  if constexpr (VEC == 4) stage_issue<LIN, PRO>(a, b, st);
-  __builtin_amdgcn_sched_barrier(0);  // the prologue's reads go out before the weights
+  if constexpr (VEC == 4) {
+    stage_issue<LIN, PRO>(a, b, st);
+    // Every wavefront's prologue reads are issued before any wavefront's weight loads: a CU's
+    // vector memory path returns data in order, so an input read queued behind weight misses
+    // would only arrive with them.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // The first tile's weights: EARLY chunks go out before the prologue (enough to keep HBM busy
+  // while it runs, without stalling the wavefront on a long run of issues), the rest after it.
+  constexpr int EARLY = VEC == 4 ? early_chunks(TAPS) : NCH;
   int tile = wg;
   float w[NCH][TAPS][VEC];
-  {
-    const int row = tile * rpt + gid;
+  const int row0 = tile * rpt + gid;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int cv = lg + j * a.tpr;
-      if (j < a.nch) load_chunk<K, VEC, RES>(a, row, cv, cv < nv && row < a.oc, w[j]);
-    }
+  for (int j = 0; j < (EARLY < NCH ? EARLY : NCH); ++j) {
+    const int cv = lg + j * a.tpr;
+    load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j]);
   }
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (VEC == 4) stage_finish<LIN, PRO>(a, b, wg, st, xs, gmean, ginv);
+#pragma unroll
+  for (int j = EARLY; j < NCH; ++j) {
+    const int cv = lg + j * a.tpr;
+    load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j]);
+  }
 
   const int waves = a.tpr / kWave;
   const int wig = lg / kWave;
@@ -434,7 +495,8 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
         }
       }
       // Refill this chunk's registers with the next tile's weights.
-      if (more && j < a.nch) load_chunk<K, VEC, RES>(a, nrow, cv, cv < nv && nrow < a.oc, w[j]);
+      load_chunk<K, VEC, RES, BF16>(a, wr, rr, nrow, cv, more && j < a.nch && cv < nv && nrow < a.oc,
+                                    w[j]);
     }
 
     rs_step<V, 32>(acc, lane);
@@ -463,6 +525,24 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
       else
         a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + lg - LOUT] = sum + a.rbias[row];
     }
+  }
+}
+
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
+__global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
+  constexpr int V = RES ? 2 * lout_of(MODE, LIN) : lout_of(MODE, LIN);
+  static_assert(V <= kWave, "one reduced value per lane");
+  extern __shared__ float4 xs4[];
+  __shared__ float gmean[kMaxGroups], ginv[kMaxGroups];
+  __shared__ float red[2 * (kThreads / kWave) * V];
+  float* xs = reinterpret_cast<float*>(xs4);
+  if constexpr (VEC == 4) {
+    if (a.bf16)
+      conv_body<MODE, K, LIN, VEC, PRO, RES, true>(a, xs, gmean, ginv, red);
+    else
+      conv_body<MODE, K, LIN, VEC, PRO, RES, false>(a, xs, gmean, ginv, red);
+  } else {
+    conv_body<MODE, K, LIN, VEC, PRO, RES, false>(a, xs, gmean, ginv, red);
   }
 }
 
