@@ -8,9 +8,17 @@ benchmark is one tick.  Also reported: host-to-host p50/p99 through the host-poi
 (PCIe-inclusive, never ``value``), actions/sec at batch 256, the HBM roofline of the tick, and the
 CPU oracle timed on this host's cores.
 
-Roofline: algorithmic bytes of a tick = all U-Net weights once per U-Net evaluation
-(1,006,026,968 bytes x 10 = 10.06 GB); ``achieved`` = those bytes / the device time of one
-sampling-graph replay (hipEvents recorded on the engine's stream around the replay).
+Roofline (``roofline``): the dominant kernel of the tick, i.e. the fused convolution shape with
+the largest device time per U-Net evaluation (the 2048<-2048, K=5, L=4 convolution with the
+GroupNorm+Mish+FiLM prologue, 4 launches per evaluation).  Its algorithmic bytes per launch are
+its weights and biases once plus its input/output activations and per-channel parameters once
+(83.9 MB); ``achieved`` = those bytes / the mean launch duration, timed with hipEvents on the
+engine's stream over launches that cycle through its distinct layers (336 MB of weights, more
+than the 256 MB MALL, as in a tick).  ``tick_roofline`` gives the same ratio for a whole tick:
+all U-Net weights once per evaluation (1,006,047,844 B x 10) / the device time of one graph
+replay.  ``traffic`` is the HBM bytes per launch measured with rocprofv3 PMC counters (read from
+the committed summary when present).  ``python bench.py --roofline-only`` runs just that kernel
+loop (plus a 256 MiB copy used to calibrate the counters) for profiling.
 """
 
 from __future__ import annotations
@@ -76,6 +84,63 @@ def unet_bytes_and_flops(spec, batch: int = 1):
     return weight_bytes, flops * batch
 
 
+DOMINANT_SHAPE = "[2048<-2048 K5 L4 film]"
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "conv_film_2048x2048_L4_pusht_traffic.txt")
+
+
+def shape_of(name: str) -> str:
+    return name[name.index("["):] if "[" in name else name
+
+
+def conv_breakdown(eng, iters: int = 50):
+    """Mean launch time of every convolution shape of one U-Net evaluation (each shape's distinct
+    layers launched round-robin) and its share of an evaluation."""
+    convs = eng.convolutions()
+    groups = {}
+    for c in convs:
+        groups.setdefault(shape_of(c["name"]), []).append(c)
+    rows = []
+    for shape, cs in groups.items():
+        us = eng.time_convolutions([c["index"] for c in cs], batch=1, iters=iters)
+        nbytes = cs[0]["weight_bytes"] + cs[0]["sample_bytes"]
+        rows.append({"shape": shape, "launches_per_nfe": len(cs), "us_per_launch": round(us, 3),
+                     "us_per_nfe": round(us * len(cs), 2), "bytes_per_launch": nbytes,
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "indices": [c["index"] for c in cs]})
+    rows.sort(key=lambda r: -r["us_per_nfe"])
+    return rows
+
+
+def dominant_roofline(eng, iters: int):
+    """Live measurement of the dominant convolution (hipEvents around `iters` rounds)."""
+    convs = [c for c in eng.convolutions() if shape_of(c["name"]) == DOMINANT_SHAPE]
+    if not convs:
+        return None
+    idx = [c["index"] for c in convs]
+    us = eng.time_convolutions(idx, batch=1, iters=iters)
+    nbytes = convs[0]["weight_bytes"] + convs[0]["sample_bytes"]
+    achieved = nbytes / (us * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_PROFILE):
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":", 1)[1].strip())
+    return {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "kernel": "conv_kernel<kConvSame, K=5, LIN=4, VEC=4, kProFilm, RES=false> "
+                  + DOMINANT_SHAPE,
+        "algorithmic_bytes_per_launch": nbytes,
+        "us_per_launch": round(us, 3),
+        "launches_timed": iters * len(idx),
+        "layers_cycled": [c["name"] for c in convs],
+    }
+
+
 def percentile(xs, q):
     import numpy as np
 
@@ -103,7 +168,7 @@ def cpu_baseline(path, spec, budget_s: float):
 
     cond, noise = ck.inputs(spec)
     out = {}
-    for label, threads in (("threads1", 0), ("all_cores", os.cpu_count() or 1)):
+    for label, threads in (("threads1", 0), ("all_cores", min(os.cpu_count() or 1, 16))):
         o = oracle.Oracle(path, threads=threads if threads > 1 else 0)
         o.sample(cond[0], noise[0], 10)  # warmup (first-touch of the weights)
         times = []
@@ -128,6 +193,10 @@ def main():
     ap.add_argument("--large-steps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--roofline-iters", type=int, default=200,
+                    help="rounds over the dominant convolution's layers")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant-kernel loop and a 256 MiB calibration copy")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -150,6 +219,15 @@ def main():
 
     eng = flowedge_amd.Engine(path)
     dev = torch.device("cuda:0")
+    if args.roofline_only:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written per launch
+        torch.cuda.synchronize()
+        roof = dominant_roofline(eng, args.roofline_iters)
+        print(json.dumps({"roofline": roof}), flush=True)
+        return
     cond, noise = ck.inputs(spec, batch=1)
     d_cond = torch.from_numpy(cond).to(dev)
     d_noise = torch.from_numpy(noise).to(dev)
@@ -217,6 +295,12 @@ def main():
         large["frac_of_fp32_mfma_peak"] = large["tflops"] / FP32_MFMA_PEAK_TFLOPS
         print(f"[bench] B={B} DDIM-10 tick p50 {bp50:.2f} ms", file=sys.stderr, flush=True)
 
+    breakdown = conv_breakdown(eng)
+    for r in breakdown:
+        print(f"[bench] {r['shape']:34s} x{r['launches_per_nfe']}  {r['us_per_launch']:8.2f} us"
+              f"  {r['gbs']:7.1f} GB/s  {r['us_per_nfe']:8.1f} us/NFE", file=sys.stderr, flush=True)
+    roof = dominant_roofline(eng, args.roofline_iters)
+
     achieved = tick_bytes / (dev_p50 / 1e3) / 1e9
     result = {
         "metric": METRIC,
@@ -247,16 +331,17 @@ def main():
         "actions_per_sec_b1": round(spec.horizon / (p50 / 1e3), 1),
         "actions_per_sec_definition": "batch * horizon / p50 tick seconds",
         "large_batch": large,
-        "roofline": {
+        "roofline": roof,
+        "tick_roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
             "kernel": "sampling tick (one hipGraph replay: 10 U-Net evaluations + updates)",
             "algorithmic_bytes_per_launch": tick_bytes,
         },
+        "conv_breakdown_b1": [{k: v for k, v in r.items() if k != "indices"} for r in breakdown],
         "finite": bool(np.all(np.isfinite(action))),
     }
     if not args.no_cpu:

@@ -32,7 +32,8 @@ EXPORTS = [
     "fe_engine_sample_diffusion_batch", "fe_engine_sample_condition_batch",
     "fe_engine_diffusion_denoise_batch", "fe_engine_sample_device", "fe_engine_prepare",
     "fe_engine_max_batch", "fe_engine_device_bytes", "fe_device_alloc_count",
-    "fe_engine_last_device_ms",
+    "fe_engine_last_device_ms", "fe_engine_conv_count", "fe_engine_conv_info",
+    "fe_engine_time_convs",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -104,6 +105,11 @@ def lib():
     L.fe_device_alloc_count.restype = u64
     L.fe_engine_last_device_ms.restype = ctypes.c_float
     L.fe_engine_last_device_ms.argtypes = [vp]
+    L.fe_engine_conv_count.argtypes = [vp, ctypes.POINTER(sz)]
+    L.fe_engine_conv_info.argtypes = [vp, sz, ctypes.c_char_p, sz, ctypes.POINTER(u64),
+                                      ctypes.POINTER(u64)]
+    L.fe_engine_time_convs.argtypes = [vp, ctypes.POINTER(sz), sz, sz, sz,
+                                       ctypes.POINTER(ctypes.c_float)]
     _lib = L
     return L
 
@@ -283,3 +289,28 @@ class Engine:
 
     def prepare(self, kind: int, batch: int, steps: int, mode: int) -> None:
         self._check(lib().fe_engine_prepare(self._h, kind, batch, steps, mode))
+
+    def convolutions(self) -> list[dict]:
+        """The fused convolutions of one U-Net evaluation in launch order: name and algorithmic
+        bytes (weights + biases per launch, activations + per-channel parameters per sample)."""
+        L = lib()
+        n = ctypes.c_size_t()
+        self._check(L.fe_engine_conv_count(self._h, ctypes.byref(n)))
+        out = []
+        buf = ctypes.create_string_buffer(256)
+        wb, sb = ctypes.c_uint64(), ctypes.c_uint64()
+        for i in range(n.value):
+            self._check(L.fe_engine_conv_info(self._h, i, buf, 256, ctypes.byref(wb),
+                                              ctypes.byref(sb)))
+            out.append({"index": i, "name": buf.value.decode(), "weight_bytes": wb.value,
+                        "sample_bytes": sb.value})
+        return out
+
+    def time_convolutions(self, indices, batch: int = 1, iters: int = 100) -> float:
+        """Mean device time (microseconds) of one launch of the given convolutions, launched
+        round-robin on the engine's stream."""
+        idx = (ctypes.c_size_t * len(indices))(*indices)
+        us = ctypes.c_float()
+        self._check(lib().fe_engine_time_convs(self._h, idx, len(indices), batch, iters,
+                                               ctypes.byref(us)))
+        return float(us.value)

@@ -253,6 +253,20 @@ struct FeEngine {
 
   std::list<GraphEntry> graphs;  // most recently used first
 
+  // Diagnostics: every fused convolution of one U-Net evaluation, recorded from an eager run.
+  struct ConvRecord {
+    std::string name;
+    fe::hip::ConvOp op;
+    bool has_res = false;
+    fe::hip::ConvOp res;
+    fe::hip::ConvInput in;
+    fe::hip::View y, yr;
+    std::uint64_t weight_bytes = 0;  // weights + biases
+    std::uint64_t sample_bytes = 0;  // activations and per-channel parameters, per sample
+  };
+  std::vector<ConvRecord> conv_records;
+  bool recording = false;
+
   template <typename T = float>
   T* ptr(std::size_t off) const {
     return reinterpret_cast<T*>(arena + off);
@@ -615,6 +629,46 @@ void bind_all(FeEngine& e) {
     if (fe_st_ != hipSuccess) return fe_st_; \
   } while (0)
 
+// Launches one fused convolution; while recording, also keeps its arguments and algorithmic
+// bytes (each weight and bias once, each activation and per-channel parameter once per sample).
+hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
+                const fe::hip::ConvOp* res, const fe::hip::ConvInput& in, fe::hip::View y,
+                fe::hip::View yr, int batch, hipStream_t s) {
+  if (e.recording) {
+    FeEngine::ConvRecord r;
+    const char* kind = !in.norm ? "plain" : (in.film_time != nullptr ? "film" : "resid");
+    const char* mode = op.mode == fe::hip::kConvSame ? "" : (op.mode == fe::hip::kConvDown ? " down" : " up");
+    char shape[128];
+    std::snprintf(shape, sizeof shape, " [%d<-%d K%d L%d%s %s%s]", op.oc, op.ic, op.k, op.lin, mode,
+                  kind, res != nullptr ? " +1x1" : "");
+    r.name = site + shape;
+    r.op = op;
+    r.has_res = res != nullptr;
+    if (res != nullptr) r.res = *res;
+    r.in = in;
+    r.y = y;
+    r.yr = yr;
+    const std::uint64_t es = op.bf16 ? 2 : 4;
+    r.weight_bytes = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * es + op.oc * 4ull;
+    std::uint64_t sb = static_cast<std::uint64_t>(op.ic) * op.lin * 4 +
+                       static_cast<std::uint64_t>(op.oc) * op.lout * 4;
+    if (res != nullptr) {
+      r.weight_bytes += static_cast<std::uint64_t>(res->oc) * res->ic * (res->bf16 ? 2 : 4) +
+                        res->oc * 4ull;
+      sb += static_cast<std::uint64_t>(res->oc) * op.lout * 4;
+    }
+    if (in.norm) {
+      sb += 2ull * in.split * 4;                                   // gamma, beta
+      if (in.film_time != nullptr) sb += 4ull * in.split * 4;      // time and condition FiLM rows
+      if (in.res != nullptr) sb += static_cast<std::uint64_t>(in.split) * op.lin * 4;
+      if (in.mat != nullptr) sb += static_cast<std::uint64_t>(in.split) * op.lin * 4;
+    }
+    r.sample_bytes = sb;
+    e.conv_records.push_back(std::move(r));
+  }
+  return fe::hip::conv_fused(op, res, in, y, yr, batch, s);
+}
+
 // How the current activation tensor is read: a plain tensor, or "virtual" as
 // Y = mish(GroupNorm(src)) + res (a ResidualBlock output that is never stored whole).
 struct Act {
@@ -650,9 +704,9 @@ fe::hip::ConvInput input_of(const FeEngine& e, const Act& in, float* mat, std::i
 //   K1: [conv1 | res 1x1](prologue(input))      -> h1, r
 //   K2: conv2(FiLM(mish(GN1(h1))))               -> h2
 // and returns its output as the virtual Y = mish(GN2(h2)) + (identity ? input : r).
-hipError_t enqueue_block(FeEngine& e, const Block& b, const Act& in, int batch,
-                         const float* film_row, float* skip_mat, std::int64_t skip_stride,
-                         Act& out) {
+hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, const Act& in,
+                         int batch, const float* film_row, float* skip_mat,
+                         std::int64_t skip_stride, Act& out) {
   using namespace fe::hip;
   hipStream_t s = e.stream;
   const std::int64_t act = static_cast<std::int64_t>(b.oc * b.len);
@@ -672,8 +726,8 @@ hipError_t enqueue_block(FeEngine& e, const Block& b, const Act& in, int batch,
   }
   ConvInput ci = input_of(e, in, mat, mat_stride);
   float* r = b.identity ? nullptr : e.ptr(b.r_off);
-  FE_TRY(conv_fused(b.c1.op, b.identity ? nullptr : &b.res.op, ci, View{h1, act}, View{r, act},
-                    batch, s));
+  FE_TRY(conv(e, site + ".conv1", b.c1.op, b.identity ? nullptr : &b.res.op, ci, View{h1, act},
+              View{r, act}, batch, s));
   ConvInput c2{};
   c2.src = h1;
   c2.src_stride = act;
@@ -686,7 +740,7 @@ hipError_t enqueue_block(FeEngine& e, const Block& b, const Act& in, int batch,
   c2.film_cond = e.ptr(e.film_cond);
   c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
   c2.film_off = static_cast<int>(b.film_off);
-  FE_TRY(conv_fused(b.c2.op, nullptr, c2, View{h2, act}, View{}, batch, s));
+  FE_TRY(conv(e, site + ".conv2", b.c2.op, nullptr, c2, View{h2, act}, View{}, batch, s));
   out = Act{};
   out.virt = true;
   out.p = h2;
@@ -716,9 +770,10 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
   x.channels = static_cast<int>(c.action_dim);
   Act y;
   for (std::size_t st = 0; st < c.stages; ++st) {
-    FE_TRY(enqueue_block(e, e.down[st][0], x, batch, film_row, nullptr, 0, y));
+    const std::string stage = "down" + std::to_string(st);
+    FE_TRY(enqueue_block(e, stage + ".b0", e.down[st][0], x, batch, film_row, nullptr, 0, y));
     x = y;
-    FE_TRY(enqueue_block(e, e.down[st][1], x, batch, film_row, nullptr, 0, y));
+    FE_TRY(enqueue_block(e, stage + ".b1", e.down[st][1], x, batch, film_row, nullptr, 0, y));
     x = y;
     if (st + 1 < c.stages) {
       // Downsample1d; its prologue materialises the stage output as the skip tensor of up stage
@@ -734,7 +789,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       ConvInput ci = input_of(e, x, skip, skip_stride);
       float* out = e.ptr(e.ds_out[st]);
       const std::int64_t os = static_cast<std::int64_t>(d.op.oc) * d.op.lout;
-      FE_TRY(conv_fused(d.op, nullptr, ci, View{out, os}, View{}, batch, s));
+      FE_TRY(conv(e, stage + ".downsample", d.op, nullptr, ci, View{out, os}, View{}, batch, s));
       x = Act{};
       x.p = out;
       x.stride = os;
@@ -747,9 +802,9 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
     const Block& m0 = e.mid[0];
     float* skip = e.ptr(e.concat[0]) + m0.ic * m0.len;
     const std::int64_t skip_stride = static_cast<std::int64_t>(e.up[0][0].ic * e.up[0][0].len);
-    FE_TRY(enqueue_block(e, m0, x, batch, film_row, skip, skip_stride, y));
+    FE_TRY(enqueue_block(e, "mid0", m0, x, batch, film_row, skip, skip_stride, y));
     x = y;
-    FE_TRY(enqueue_block(e, e.mid[1], x, batch, film_row, nullptr, 0, y));
+    FE_TRY(enqueue_block(e, "mid1", e.mid[1], x, batch, film_row, nullptr, 0, y));
     x = y;
   }
   for (std::size_t u = 0; u + 1 < c.stages; ++u) {
@@ -776,8 +831,9 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       ConvInput ci = input_of(e, in, nullptr, 0);
       ci.plain = e.ptr(e.concat[u]) + half * r0.len;
       ci.plain_stride = cs;
-      FE_TRY(conv_fused(r0.c1.op, &r0.res.op, ci, View{e.ptr(r0.h1_off), act},
-                        View{e.ptr(r0.r_off), act}, batch, s2));
+      const std::string stage = "up" + std::to_string(u);
+      FE_TRY(conv(e, stage + ".b0.conv1", r0.c1.op, &r0.res.op, ci, View{e.ptr(r0.h1_off), act},
+                  View{e.ptr(r0.r_off), act}, batch, s2));
       ConvInput c2{};
       c2.src = e.ptr(r0.h1_off);
       c2.src_stride = act;
@@ -790,7 +846,8 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       c2.film_cond = e.ptr(e.film_cond);
       c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
       c2.film_off = static_cast<int>(r0.film_off);
-      FE_TRY(conv_fused(r0.c2.op, nullptr, c2, View{e.ptr(r0.h2_off), act}, View{}, batch, s2));
+      FE_TRY(conv(e, stage + ".b0.conv2", r0.c2.op, nullptr, c2, View{e.ptr(r0.h2_off), act},
+                  View{}, batch, s2));
       y = Act{};
       y.virt = true;
       y.p = e.ptr(r0.h2_off);
@@ -802,7 +859,8 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       y.channels = static_cast<int>(r0.oc);
       x = y;
     }
-    FE_TRY(enqueue_block(e, e.up[u][1], x, batch, film_row, nullptr, 0, y));
+    FE_TRY(enqueue_block(e, "up" + std::to_string(u) + ".b1", e.up[u][1], x, batch, film_row,
+                         nullptr, 0, y));
     x = y;
     // Upsample1d into the first half of the next up stage's input, or the final conv input.
     const ConvSlot& up = e.us[u];
@@ -815,7 +873,8 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       dst.stride = static_cast<std::int64_t>(c.dims[0] * c.horizon);
     }
     ConvInput ci = input_of(e, x, nullptr, 0);
-    FE_TRY(conv_fused(up.op, nullptr, ci, dst, View{}, batch, s));
+    FE_TRY(conv(e, "up" + std::to_string(u) + ".upsample", up.op, nullptr, ci, dst, View{}, batch,
+                s));
   }
   const std::int64_t fs = static_cast<std::int64_t>(c.dims[0] * c.horizon);
   float* fo = e.ptr(e.fconv_out);
@@ -823,7 +882,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
   fi.src = e.ptr(e.final_in);
   fi.src_stride = fs;
   fi.split = static_cast<int>(c.dims[0]);
-  FE_TRY(conv_fused(e.fconv.op, nullptr, fi, View{fo, fs}, View{}, batch, s));
+  FE_TRY(conv(e, "final.conv", e.fconv.op, nullptr, fi, View{fo, fs}, View{}, batch, s));
   upd.c0 = static_cast<int>(c.dims[0]);
   upd.horizon = static_cast<int>(c.horizon);
   upd.action_dim = static_cast<int>(c.action_dim);
@@ -1022,6 +1081,31 @@ int hip_fail(const char* what, hipError_t st) {
 }
 
 // Validates a sampling request (engine_runtime.cc:446-470 + extensions).
+// Records the convolutions of one U-Net evaluation (batch 1, eager, on whatever the buffers hold)
+// the first time a diagnostic asks for them.
+int ensure_conv_records(FeEngine* e) {
+  if (!e->conv_records.empty()) return FE_STATUS_OK;
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  using namespace fe::hip;
+  TimeSpec ts;
+  ts.mode = kTimesSingle;
+  ts.t0 = 0.0f;
+  UpdateOp u{};
+  u.kind = kUpdateDenoise;
+  u.out = e->ptr(e->out_action);
+  e->recording = true;
+  st = enqueue_film(*e, ts, 1, 1);
+  if (st == hipSuccess) st = enqueue_unet(*e, 1, e->ptr(e->film_table), u);
+  e->recording = false;
+  if (st == hipSuccess) st = hipStreamSynchronize(e->stream);
+  if (st != hipSuccess) {
+    e->conv_records.clear();
+    return hip_fail("Diagnostic U-Net evaluation failed", st);
+  }
+  return FE_STATUS_OK;
+}
+
 int check_sample(const FeEngine* e, int kind, std::size_t batch, std::size_t steps, int mode) {
   if (kind == 0) {
     if (e->cfg.prediction != 0) {
@@ -1514,6 +1598,84 @@ size_t fe_engine_device_bytes(const fe_engine* engine) {
 }
 
 uint64_t fe_device_alloc_count(void) { return g_device_allocs.load(); }
+
+int fe_engine_conv_count(fe_engine* engine, size_t* count) {
+  clear_error();
+  if (engine == nullptr || count == nullptr) {
+    set_error("Invalid arguments to fe_engine_conv_count");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const int rc = ensure_conv_records(engine);
+  if (rc != FE_STATUS_OK) return rc;
+  *count = engine->conv_records.size();
+  return FE_STATUS_OK;
+}
+
+int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name_capacity,
+                        uint64_t* weight_bytes, uint64_t* sample_bytes) {
+  clear_error();
+  if (engine == nullptr) {
+    set_error("Invalid arguments to fe_engine_conv_info");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const int rc = ensure_conv_records(engine);
+  if (rc != FE_STATUS_OK) return rc;
+  if (index >= engine->conv_records.size()) {
+    set_error("Convolution index out of range");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const FeEngine::ConvRecord& r = engine->conv_records[index];
+  if (name != nullptr && name_capacity > 0) {
+    const std::size_t n = std::min(name_capacity - 1, r.name.size());
+    std::memcpy(name, r.name.data(), n);
+    name[n] = '\0';
+  }
+  if (weight_bytes != nullptr) *weight_bytes = r.weight_bytes;
+  if (sample_bytes != nullptr) *sample_bytes = r.sample_bytes;
+  return FE_STATUS_OK;
+}
+
+int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, size_t batch,
+                         size_t iters, float* avg_us) {
+  clear_error();
+  if (engine == nullptr || indices == nullptr || n == 0 || iters == 0 || avg_us == nullptr ||
+      batch == 0 || batch > engine->max_batch) {
+    set_error("Invalid arguments to fe_engine_time_convs");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  FeEngine* e = engine;
+  const int rc = ensure_conv_records(e);
+  if (rc != FE_STATUS_OK) return rc;
+  for (size_t i = 0; i < n; ++i)
+    if (indices[i] >= e->conv_records.size()) {
+      set_error("Convolution index out of range");
+      return FE_STATUS_INVALID_ARGUMENT;
+    }
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  const int b = static_cast<int>(batch);
+  auto round = [&]() -> hipError_t {
+    for (size_t i = 0; i < n; ++i) {
+      const FeEngine::ConvRecord& r = e->conv_records[indices[i]];
+      const hipError_t s2 = fe::hip::conv_fused(r.op, r.has_res ? &r.res : nullptr, r.in, r.y,
+                                                r.yr, b, e->stream);
+      if (s2 != hipSuccess) return s2;
+    }
+    return hipSuccess;
+  };
+  if ((st = round()) != hipSuccess || (st = hipEventRecord(e->ev0, e->stream)) != hipSuccess)
+    return hip_fail("Convolution timing failed", st);
+  for (size_t it = 0; it < iters; ++it)
+    if ((st = round()) != hipSuccess) return hip_fail("Convolution timing failed", st);
+  float ms = 0.0f;
+  if ((st = hipEventRecord(e->ev1, e->stream)) != hipSuccess ||
+      (st = hipEventSynchronize(e->ev1)) != hipSuccess ||
+      (st = hipEventElapsedTime(&ms, e->ev0, e->ev1)) != hipSuccess)
+    return hip_fail("Convolution timing failed", st);
+  e->timed = false;  // the events no longer bracket a sampling graph
+  *avg_us = ms * 1000.0f / static_cast<float>(iters * n);
+  return FE_STATUS_OK;
+}
 
 float fe_engine_last_device_ms(const fe_engine* engine) {
   if (engine == nullptr || !engine->timed) return -1.0f;

@@ -213,6 +213,22 @@ uint64_t fe_device_alloc_count(void);
  * graph launch on the engine's stream), or -1 if none. */
 float fe_engine_last_device_ms(const fe_engine* engine);
 
+/* Diagnostics (no counterpart in the reference; for benchmarks and profiling).  The fused
+ * convolutions of one U-Net evaluation, in launch order, recorded from an eager batch-1
+ * evaluation on the engine's current buffers the first time they are asked for. */
+int fe_engine_conv_count(fe_engine* engine, size_t* count);
+
+/* Name ("site [oc<-ic Kk Llin prologue]") and algorithmic bytes of convolution `index`: weights
+ * and biases (read once per launch) and activations plus per-channel parameters (per sample). */
+int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name_capacity,
+                        uint64_t* weight_bytes, uint64_t* sample_bytes);
+
+/* Launches convolutions indices[0..n) round-robin `iters` times at `batch` on the engine's stream
+ * and returns the mean device time of one launch in microseconds (hipEvents around the loop, after
+ * one untimed round).  Outputs land in the engine's own buffers. */
+int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, size_t batch,
+                         size_t iters, float* avg_us);
+
 #ifdef __cplusplus
 }
 #endif
