@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libflowedge_amd.so")
 SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/conv_fused.hip",
-           "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip"]
+           "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip",
+           "csrc/conv_mfma.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 

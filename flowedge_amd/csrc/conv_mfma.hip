@@ -1,0 +1,459 @@
+// Batched convolution on the matrix cores (gfx950 v_mfma_f32_16x16x4f32), for sampling calls with
+// many samples.  Each convolution is an implicit GEMM
+//     Y[oc][(b, t)] = bias[oc] + sum_{k, ic} W[oc][k][ic] * X[b][ic][src(t, k)]
+// with A = the repacked weights [OC][K][IC] (row-major [OC][K*IC]) and B = the input gathered per
+// tap (src(t, k) as conv1d / ConvTranspose1d define it, zero outside the input).  The GroupNorm +
+// Mish (+ FiLM) (+ residual) prologue runs first as its own per-sample kernel (norm_act), whose
+// output the GEMM reads as a plain tensor.
+//
+// GEMM tiling: a 256-lane workgroup owns MT output channels x 128 columns (samples x output
+// positions); its four wavefronts each own (MT/2) x 64.  The K loop walks 16 input channels at a
+// time (all taps), double-buffered in LDS: the next step's weights and inputs are loaded into
+// registers while the matrix cores work on the current one.  Within a 16-channel step a lane
+// feeds the MFMA k-slot (lane / 16) with channels 4 * (lane / 16) + s over four MFMAs s, so
+// every operand read is one 16-byte LDS load.  Output positions whose input index falls in the
+// padding read a zero row.  Workgroups that share a weight tile are placed on the same XCD
+// (dispatch is round-robin over the 8 XCDs), so the tile is fetched into one L2.
+//
+// Reference semantics: conv1d diffusion_ops.cc:82-163, conv_transpose1d :165-268,
+// group_norm :270-350, film :352-377.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace fe::hip {
+namespace {
+
+using namespace dev;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMmThreads = 256;
+constexpr int kKC = 16;   // input channels per K step
+constexpr int kNT = 128;  // columns per workgroup
+constexpr int kPad = 4;   // LDS row padding (floats)
+
+__host__ __device__ constexpr int lout_for(int mode, int lin) {
+  return mode == kConvSame ? lin : (mode == kConvDown ? lin / 2 : 2 * lin);
+}
+
+struct MmArgs {
+  const void* w;
+  const float* bias;
+  float* y;
+  std::int64_t ys;
+  const float* src;
+  std::int64_t src_stride;
+  int split;
+  const float* plain;
+  std::int64_t plain_stride;
+  int oc, ic, batch;
+  int mtiles, ntiles;
+};
+
+// Input index read by output t through tap k, or -1 in the padding (t known only at run time).
+template <int MODE, int K, int LIN>
+__device__ __forceinline__ int src_at(int t, int k) {
+  if constexpr (MODE == kConvSame) {
+    const int j = t + k - K / 2;
+    return (j >= 0 && j < LIN) ? j : -1;
+  } else if constexpr (MODE == kConvDown) {
+    const int j = 2 * t + k - 1;
+    return (j >= 0 && j < LIN) ? j : -1;
+  } else {
+    const int num = t + 1 - k;  // ConvTranspose: output t = 2 * j + k - 1
+    if (num < 0 || (num & 1)) return -1;
+    const int j = num >> 1;
+    return j < LIN ? j : -1;
+  }
+}
+
+template <int MODE, int K, int LIN, int MT>
+struct MmShape {
+  static constexpr int LOUT = lout_for(MODE, LIN);
+  static constexpr int SB = kNT / LOUT;          // samples per column tile
+  static constexpr int WROW = K * kKC + kPad;    // LDS floats per weight row
+  static constexpr int XROW = kKC + kPad;        // LDS floats per (sample, position) row
+  static constexpr int ZERO = SB * LIN;          // index of the zero row
+  static constexpr int XROWS = SB * LIN + 1;
+  static constexpr int WFLOATS = MT * WROW;
+  static constexpr int XFLOATS = XROWS * XROW;
+  static constexpr int UW = MT * K * 4 / kMmThreads;  // weight float4 per lane per step
+  static constexpr int XELEMS = SB * kKC * LIN;       // input floats per step
+  static constexpr int XV = LIN >= 4 ? 4 : 1;          // vector width of input loads
+  static constexpr int UX = XELEMS / XV / kMmThreads;
+  static constexpr int WM = MT / 2, WN = kNT / 2;
+  static constexpr int TI = WM / 16, TJ = WN / 16;
+  static_assert(MT * K * 4 % kMmThreads == 0, "weight units per lane");
+  static_assert(XELEMS % (XV * kMmThreads) == 0, "input units per lane");
+};
+
+template <bool BF16>
+__device__ __forceinline__ float4 load_w4(const void* base, std::int64_t idx) {
+  if constexpr (BF16) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(base) + idx);
+    return float4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                  __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+  } else {
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+  }
+}
+
+template <int MODE, int K, int LIN, bool BF16, int MT>
+__global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
+  using S = MmShape<MODE, K, LIN, MT>;
+  extern __shared__ float4 lds4[];
+  float* Ws = reinterpret_cast<float*>(lds4);  // [2][WFLOATS]
+  float* Xs = Ws + 2 * S::WFLOATS;             // [2][XFLOATS]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // Tile index, grouped so that the workgroups on one XCD share weight tiles.
+  int id = blockIdx.x;
+  const int total = a.mtiles * a.ntiles;
+  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  const int mt = id / a.ntiles, nt = id - mt * a.ntiles;
+  const int m0 = mt * MT;
+  const int b0 = nt * S::SB;
+  const int nsteps = a.ic / kKC;
+
+  // Zero rows of both input buffers (never overwritten).
+  if (tid < 2 * kKC) Xs[(tid / kKC) * S::XFLOATS + S::ZERO * S::XROW + (tid % kKC)] = 0.0f;
+
+  float4 wreg[S::UW];
+  float4 xreg[S::UX > 0 ? S::UX : 1];
+  float xs1[S::XV == 1 ? S::UX : 1];
+  auto load_step = [&](int step) {
+    const int ic0 = step * kKC;
+#pragma unroll
+    for (int r = 0; r < S::UW; ++r) {
+      const int u = tid + r * kMmThreads;
+      const int m = u / (K * 4), rem = u - m * (K * 4);
+      const int k = rem >> 2, q = rem & 3;
+      const int oc = m0 + m;
+      wreg[r] = oc < a.oc ? load_w4<BF16>(a.w, (static_cast<std::int64_t>(oc) * K + k) * a.ic + ic0 + 4 * q)
+                          : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int r = 0; r < S::UX; ++r) {
+      const int u = tid + r * kMmThreads;
+      if constexpr (S::XV == 4) {
+        const int bl = u / (4 * LIN), v = u - bl * (4 * LIN);
+        const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
+        const int b = b0 + bl, c = ic0 + ch;
+        float4 val = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (b < a.batch) {
+          const float* p = c < a.split ? a.src + b * a.src_stride + static_cast<std::int64_t>(c) * LIN
+                                       : a.plain + b * a.plain_stride +
+                                             static_cast<std::int64_t>(c - a.split) * LIN;
+          val = *reinterpret_cast<const float4*>(p + t4);
+        }
+        xreg[r] = val;
+      } else {
+        const int bl = u / (kKC * LIN), v = u - bl * (kKC * LIN);
+        const int ch = v / LIN, t = v - ch * LIN;
+        const int b = b0 + bl, c = ic0 + ch;
+        float val = 0.0f;
+        if (b < a.batch)
+          val = c < a.split ? a.src[b * a.src_stride + static_cast<std::int64_t>(c) * LIN + t]
+                            : a.plain[b * a.plain_stride + static_cast<std::int64_t>(c - a.split) * LIN + t];
+        xs1[r] = val;
+      }
+    }
+  };
+  auto store_step = [&](int buf) {
+    float* W = Ws + buf * S::WFLOATS;
+    float* X = Xs + buf * S::XFLOATS;
+#pragma unroll
+    for (int r = 0; r < S::UW; ++r) {
+      const int u = tid + r * kMmThreads;
+      const int m = u / (K * 4), rem = u - m * (K * 4);
+      const int k = rem >> 2, q = rem & 3;
+      *reinterpret_cast<float4*>(W + m * S::WROW + k * kKC + 4 * q) = wreg[r];
+    }
+#pragma unroll
+    for (int r = 0; r < S::UX; ++r) {
+      const int u = tid + r * kMmThreads;
+      if constexpr (S::XV == 4) {
+        const int bl = u / (4 * LIN), v = u - bl * (4 * LIN);
+        const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
+        float* row = X + (bl * LIN + t4) * S::XROW + ch;
+        row[0] = xreg[r].x;
+        row[S::XROW] = xreg[r].y;
+        row[2 * S::XROW] = xreg[r].z;
+        row[3 * S::XROW] = xreg[r].w;
+      } else {
+        const int bl = u / (kKC * LIN), v = u - bl * (kKC * LIN);
+        const int ch = v / LIN, t = v - ch * LIN;
+        X[(bl * LIN + t) * S::XROW + ch] = xs1[r];
+      }
+    }
+  };
+
+  // Per-lane input row of every (column tile j, tap k): fixed for the whole K loop.
+  const int wr = wave >> 1, wc = wave & 1;
+  const int kq = lane >> 4, l16 = lane & 15;
+  int xrow[S::TJ][K];
+#pragma unroll
+  for (int j = 0; j < S::TJ; ++j) {
+    const int col = wc * S::WN + 16 * j + l16;
+    const int bl = col / S::LOUT, t = col - bl * S::LOUT;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int ti = src_at<MODE, K, LIN>(t, k);
+      xrow[j][k] = (ti >= 0 ? bl * LIN + ti : S::ZERO) * S::XROW + 4 * kq;
+    }
+  }
+  const int arow = (wr * S::WM + l16) * S::WROW + 4 * kq;
+
+  floatx4 acc[S::TI][S::TJ];
+#pragma unroll
+  for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < S::TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    if (step + 1 < nsteps) load_step(step + 1);
+    const float* W = Ws + buf * S::WFLOATS;
+    const float* X = Xs + buf * S::XFLOATS;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      float4 av[S::TI], bv[S::TJ];
+#pragma unroll
+      for (int i = 0; i < S::TI; ++i)
+        av[i] = *reinterpret_cast<const float4*>(W + arow + i * 16 * S::WROW + k * kKC);
+#pragma unroll
+      for (int j = 0; j < S::TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(X + xrow[j][k]);
+#pragma unroll
+      for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < S::TJ; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
+        }
+    }
+    if (step + 1 < nsteps) store_step(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds rows 4 * (lane / 16) + e of each 16x16 tile, column lane % 16.
+#pragma unroll
+  for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
+      if (oc >= a.oc) continue;
+      const float bias = a.bias[oc];
+#pragma unroll
+      for (int j = 0; j < S::TJ; ++j) {
+        const int col = wc * S::WN + 16 * j + l16;
+        const int bl = col / S::LOUT, t = col - bl * S::LOUT;
+        const int b = b0 + bl;
+        if (b < a.batch)
+          a.y[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] = acc[i][j][e] + bias;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Per-sample prologue: dst = mish(GN(src)) [* scale + shift] [+ res] for the `split` channels.
+// ---------------------------------------------------------------------------------------------
+constexpr int kNaThreads = 512;
+constexpr int kNaMaxFloats = 8192;
+
+template <int LIN>
+__global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, float* dst,
+                                                              std::int64_t dst_stride) {
+  constexpr int QN = kNaMaxFloats / 4 / kNaThreads;
+  __shared__ double ps[kNaMaxFloats / 4], pq[kNaMaxFloats / 4];
+  __shared__ float gmean[32], ginv[32];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nqn = in.split * LIN / 4;
+  const int npg = in.split / in.groups * LIN / 4;
+  const float* src = in.src + b * in.src_stride;
+  float4 x[QN], r[QN];
+#pragma unroll
+  for (int m = 0; m < QN; ++m) {
+    const int q = tid + m * kNaThreads;
+    x[m] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    r[m] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (q < nqn) {
+      x[m] = *reinterpret_cast<const float4*>(src + 4 * q);
+      if (in.res != nullptr) r[m] = *reinterpret_cast<const float4*>(in.res + b * in.res_stride + 4 * q);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < QN; ++m) {
+    const int q = tid + m * kNaThreads;
+    if (q < nqn) {
+      const double d0 = x[m].x, d1 = x[m].y, d2 = x[m].z, d3 = x[m].w;
+      ps[q] = (d0 + d1) + (d2 + d3);
+      pq[q] = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+  }
+  __syncthreads();
+  const int wave = tid / kWave, lane = tid & (kWave - 1);
+  for (int g = wave; g < in.groups; g += kNaThreads / kWave) {
+    double s = 0.0, sq = 0.0;
+    for (int i = lane; i < npg; i += kWave) {
+      s += ps[g * npg + i];
+      sq += pq[g * npg + i];
+    }
+    s = wave_sum(s);
+    sq = wave_sum(sq);
+    if (lane == 0) {
+      const double n = 4.0 * npg;
+      const double mean = s / n;
+      const double var = fmax(0.0, sq / n - mean * mean);
+      gmean[g] = static_cast<float>(mean);
+      ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
+    }
+  }
+  __syncthreads();
+  const float* ft = in.film_time != nullptr ? in.film_time + in.film_off : nullptr;
+  const float* fc = in.film_time != nullptr ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
+#pragma unroll
+  for (int m = 0; m < QN; ++m) {
+    const int q = tid + m * kNaThreads;
+    if (q >= nqn) continue;
+    const int g = q / npg;
+    const float mean = gmean[g], inv = ginv[g];
+    float v[4] = {x[m].x, x[m].y, x[m].z, x[m].w};
+    const float rr[4] = {r[m].x, r[m].y, r[m].z, r[m].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = (4 * q + i) / LIN;
+      float val = mish_fast(fmaf(v[i] - mean, inv * in.gamma[c], in.beta[c]));
+      if (ft != nullptr) val = fmaf(ft[c] + fc[c], val, ft[in.split + c] + fc[in.split + c]);
+      v[i] = val + rr[i];
+    }
+    *reinterpret_cast<float4*>(dst + b * dst_stride + 4 * q) = float4{v[0], v[1], v[2], v[3]};
+  }
+}
+
+template <int MODE, int K, int LIN, bool BF16, int MT>
+hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
+  using S = MmShape<MODE, K, LIN, MT>;
+  const std::size_t smem = (2 * S::WFLOATS + 2 * S::XFLOATS) * sizeof(float);
+  auto fn = conv_mfma_kernel<MODE, K, LIN, BF16, MT>;
+  static bool raised = false;
+  if (!raised && smem > 48 * 1024) {
+    const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(smem));
+    if (st != hipSuccess) return st;
+    raised = true;
+  }
+  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles), dim3(kMmThreads), smem, s, a);
+  return hipGetLastError();
+}
+
+template <int MODE, int K, int LIN, bool BF16>
+hipError_t by_mt(int mt, const MmArgs& a, hipStream_t s) {
+  return mt == 128 ? launch_mm<MODE, K, LIN, BF16, 128>(a, s) : launch_mm<MODE, K, LIN, BF16, 64>(a, s);
+}
+
+template <int MODE, int K, bool BF16>
+hipError_t by_lin_mm(int lin, int mt, const MmArgs& a, hipStream_t s) {
+  switch (lin) {
+    case 1:
+      if constexpr (MODE != kConvDown) return by_mt<MODE, K, 1, BF16>(mt, a, s);
+      break;
+    case 2: return by_mt<MODE, K, 2, BF16>(mt, a, s);
+    case 4: return by_mt<MODE, K, 4, BF16>(mt, a, s);
+    case 8: return by_mt<MODE, K, 8, BF16>(mt, a, s);
+    case 16:
+      if constexpr (MODE != kConvTranspose) return by_mt<MODE, K, 16, BF16>(mt, a, s);
+      break;
+    default: break;
+  }
+  return hipErrorInvalidValue;
+}
+
+template <bool BF16>
+hipError_t by_kernel_mm(const ConvOp& op, int mt, const MmArgs& a, hipStream_t s) {
+  if (op.mode == kConvSame) {
+    switch (op.k) {
+      case 1: return by_lin_mm<kConvSame, 1, BF16>(op.lin, mt, a, s);
+      case 3: return by_lin_mm<kConvSame, 3, BF16>(op.lin, mt, a, s);
+      case 5: return by_lin_mm<kConvSame, 5, BF16>(op.lin, mt, a, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (op.mode == kConvDown && op.k == 3) return by_lin_mm<kConvDown, 3, BF16>(op.lin, mt, a, s);
+  if (op.mode == kConvTranspose && op.k == 4)
+    return by_lin_mm<kConvTranspose, 4, BF16>(op.lin, mt, a, s);
+  return hipErrorInvalidValue;
+}
+
+bool lin_mm_ok(int mode, int lin) {
+  if (lin != 1 && lin != 2 && lin != 4 && lin != 8 && lin != 16) return false;
+  if (mode == kConvDown && lin < 2) return false;
+  if (mode == kConvTranspose && lin > 8) return false;
+  return true;
+}
+
+}  // namespace
+
+bool conv_mfma_supported(const ConvOp& op, int split) {
+  if (!lin_mm_ok(op.mode, op.lin) || op.lout != lout_for(op.mode, op.lin)) return false;
+  if (op.ic % kKC != 0 || split % kKC != 0 || split > op.ic || op.oc <= 0) return false;
+  if (op.mode == kConvSame) return op.k == 1 || op.k == 3 || op.k == 5;
+  if (op.mode == kConvDown) return op.k == 3;
+  return op.mode == kConvTranspose && op.k == 4;
+}
+
+hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
+                     const float* plain, std::int64_t plain_stride, View y, int batch,
+                     hipStream_t stream) {
+  if (!conv_mfma_supported(op, split) || batch <= 0) return hipErrorInvalidValue;
+  if (split < op.ic && plain == nullptr) return hipErrorInvalidValue;
+  MmArgs a{};
+  a.w = op.w;
+  a.bias = op.b;
+  a.y = y.p;
+  a.ys = y.stride;
+  a.src = src;
+  a.src_stride = src_stride;
+  a.split = split;
+  a.plain = plain;
+  a.plain_stride = plain_stride;
+  a.oc = op.oc;
+  a.ic = op.ic;
+  a.batch = batch;
+  const int sb = kNT / op.lout;
+  a.ntiles = (batch + sb - 1) / sb;
+  // 128-row tiles when they alone give every CU a workgroup, else 64-row tiles.
+  int mt = 128;
+  if (((op.oc + 127) / 128) * a.ntiles < 256) mt = 64;
+  a.mtiles = (op.oc + mt - 1) / mt;
+  return op.bf16 ? by_kernel_mm<true>(op, mt, a, stream) : by_kernel_mm<false>(op, mt, a, stream);
+}
+
+hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,
+                    hipStream_t stream) {
+  if (!in.norm || batch <= 0 || in.groups <= 0 || in.groups > 32 || in.split % in.groups != 0 ||
+      (in.split / in.groups * lin) % 4 != 0 || in.split * lin > kNaMaxFloats)
+    return hipErrorInvalidValue;
+  switch (lin) {
+    case 1: hipLaunchKernelGGL(norm_act_kernel<1>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
+    case 2: hipLaunchKernelGGL(norm_act_kernel<2>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
+    case 4: hipLaunchKernelGGL(norm_act_kernel<4>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
+    case 8: hipLaunchKernelGGL(norm_act_kernel<8>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
+    case 16: hipLaunchKernelGGL(norm_act_kernel<16>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fe::hip

@@ -53,6 +53,7 @@ bool env_flag(const char* name) {
 
 constexpr unsigned kMaxPoolThreads = 8;  // engine_runtime.h:39
 constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
+constexpr std::size_t kMaxNormFloats = 8192;  // width * length of any normalised activation
 constexpr std::size_t kFinalNormGroups = 8;  // diffusion.cc:28
 constexpr std::size_t kAlign = 256;
 
@@ -250,6 +251,8 @@ struct FeEngine {
   std::size_t x_state = 0, x_in = 0, k_stages = 0;
   std::size_t in_cond = 0, in_noise = 0, out_action = 0, seed_dev = 0;
   std::size_t final_in = 0;
+  std::size_t xnorm = 0;       // batched path: normalised input of one convolution [B][8192]
+  std::size_t mfma_batch = 8;  // batches of at least this many samples use the matrix cores
 
   std::list<GraphEntry> graphs;  // most recently used first
 
@@ -469,6 +472,7 @@ struct Builder {
       for (int k = 0; k < 2; ++k) acts(e.up[u][k]);
     e.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
     e.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
+    e.xnorm = plan.take(B * kMaxNormFloats * 4);
     return true;
   }
 };
@@ -666,7 +670,26 @@ hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
     r.sample_bytes = sb;
     e.conv_records.push_back(std::move(r));
   }
-  return fe::hip::conv_fused(op, res, in, y, yr, batch, s);
+  using namespace fe::hip;
+  if (static_cast<std::size_t>(batch) >= e.mfma_batch && conv_mfma_supported(op, in.split) &&
+      (res == nullptr || conv_mfma_supported(*res, in.split))) {
+    // Many samples: the prologue as its own pass, then implicit GEMMs on the matrix cores.
+    const float* src = in.src;
+    std::int64_t ss = in.src_stride;
+    if (in.norm) {
+      float* dst = in.mat != nullptr ? in.mat : e.ptr(e.xnorm);
+      const std::int64_t ds =
+          in.mat != nullptr ? in.mat_stride : static_cast<std::int64_t>(in.split) * op.lin;
+      FE_TRY(norm_act(in, op.lin, dst, ds, batch, s));
+      src = dst;
+      ss = ds;
+    }
+    FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, s));
+    if (res != nullptr)
+      FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, s));
+    return hipSuccess;
+  }
+  return conv_fused(op, res, in, y, yr, batch, s);
 }
 
 // How the current activation tensor is read: a plain tensor, or "virtual" as
@@ -1183,6 +1206,16 @@ int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, st
   return FE_STATUS_OK;
 }
 
+// Smallest batch that runs the convolutions on the matrix cores (FLOWEDGE_MFMA_BATCH, default 8;
+// a value above the max batch keeps every batch on the weight-streaming kernels).
+std::size_t env_mfma_batch() {
+  const char* v = std::getenv("FLOWEDGE_MFMA_BATCH");
+  if (v == nullptr || *v == '\0') return 8;
+  char* end = nullptr;
+  const unsigned long n = std::strtoul(v, &end, 10);
+  return (end && *end == '\0' && n > 0) ? n : 8;
+}
+
 std::size_t env_max_batch() {
   const char* v = std::getenv("FLOWEDGE_MAX_BATCH");
   if (v == nullptr || *v == '\0') return 256;
@@ -1219,6 +1252,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     return nullptr;
   }
   e->max_batch = env_max_batch();
+  e->mfma_batch = env_mfma_batch();
   if (e->max_batch == 0) {
     set_error("FLOWEDGE_MAX_BATCH must be an integer from 1 through 65535");
     return nullptr;

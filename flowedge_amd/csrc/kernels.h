@@ -75,6 +75,18 @@ hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& i
 // `split` channels from the prologue source, `norm` with a GroupNorm prologue.
 bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm);
 
+// Batched path (matrix cores).  y = conv(x) + bias with x a plain tensor: channels [0, split)
+// from `src`, the rest from `plain`.  Needs ic and split to be multiples of 16.
+bool conv_mfma_supported(const ConvOp& op, int split);
+hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
+                     const float* plain, std::int64_t plain_stride, View y, int batch,
+                     hipStream_t stream);
+
+// The prologue of a ConvInput with `norm` on its own: dst[b][0 : split*lin) =
+// mish(GN(src)) [* scale + shift] [+ res], per sample.
+hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,
+                    hipStream_t stream);
+
 // Timestep of the n-th U-Net evaluation of a sampling call, derived on the device:
 //   kTimesSingle: t = t0
 //   kTimesDiffusion: t_n = (steps - 1 - n) * ratio         (diffusion.cc:984-990)

@@ -3,8 +3,10 @@
 Tolerances (written per test): fp32 checkpoints must match within max |err| <= 1e-4 in action
 units (action scale (max - min)/2 = 1 for the synthetic range [-1, 1]); BF16-weight checkpoints
 are held to the same 1e-4 here because the oracle runs on the identical BF16-rounded values
-(the contract bound for BF16 variants is 2e-2).  Batched calls must equal independent batch-1
-calls bit for bit.
+(the contract bound for BF16 variants is 2e-2).  Batches below the matrix-core threshold
+(FLOWEDGE_MFMA_BATCH, default 8) run the batch-1 kernels and must equal independent batch-1
+calls bit for bit; larger batches run implicit GEMMs on the matrix cores (another summation
+order) and are held to the oracle per sample at the same 1e-4.
 """
 
 from __future__ import annotations
@@ -248,3 +250,68 @@ def test_flow_full_size(ckpt_dir):
             err = maxerr(out, want)
             say(f"flow {method} max err {err:.3e}")
             assert err <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# Batched path: the convolutions run as implicit GEMMs on the matrix cores (batch >= 8).
+# ---------------------------------------------------------------------------------------------
+def test_tiny_batched_mfma(tiny_engine, tiny_oracle):
+    spec = ck.SPECS["tiny"]
+    B = 19  # not a multiple of any column tile: exercises the sample masking
+    cond, noise = ck.inputs(spec, batch=B)
+    say(f"tiny DDIM-10 / DDPM / denoise batch={B} (matrix cores)")
+    got = tiny_engine.sample_diffusion_batch(cond, noise, steps=10)
+    want = tiny_oracle.sample_batch(cond, noise, 10, workers=8)
+    assert maxerr(got, want) <= TOL
+    got = tiny_engine.sample_diffusion_batch(cond, noise, steps=10, scheduler="ddpm", seed=7)
+    want = tiny_oracle.sample_batch(cond, noise, 10, 0, 1, 7, workers=8)
+    assert maxerr(got, want) <= TOL
+    eps = tiny_engine.diffusion_denoise_batch(cond, noise, 50.0)
+    for b in (0, 7, 18):
+        assert maxerr(eps[b], tiny_oracle.denoise(cond[b], noise[b], 50.0)) <= TOL
+    # Within tolerance of independent batch-1 calls (different summation order).
+    for b in (0, 18):
+        assert maxerr(got[b], tiny_engine.sample_diffusion(cond[b], noise[b], steps=10,
+                                                           scheduler="ddpm", seed=7)) <= 2 * TOL
+
+
+def test_pusht_batched_mfma(pusht):
+    spec = ck.SPECS["pusht"]
+    B = 16
+    cond, noise = ck.inputs(spec, batch=B)
+    o = oracle.Oracle(pusht, threads=0)
+    say(f"pusht DDIM-10 batch={B} (matrix cores)")
+    with flowedge_amd.Engine(pusht) as e:
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+    want = o.sample_batch(cond, noise, 10, workers=8)
+    err = maxerr(got, want)
+    say(f"pusht batch={B} max err {err:.3e}")
+    assert err <= TOL
+
+
+def test_bimanual_bf16_batched_mfma(ckpt_dir):
+    spec = ck.SPECS["bimanual"]
+    path = ck.cached_checkpoint("bimanual", ckpt_dir)
+    B = 12
+    cond, noise = ck.inputs(spec, batch=B)
+    o = oracle.Oracle(path, threads=0)
+    say(f"bimanual bf16 DDIM-10 batch={B} (matrix cores, length-2 stage)")
+    with flowedge_amd.Engine(path) as e:
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+    err = maxerr(got, o.sample_batch(cond, noise, 10, workers=8))
+    say(f"bimanual batch={B} max err {err:.3e}")
+    assert err <= TOL
+
+
+def test_flow_batched_mfma(ckpt_dir):
+    spec = ck.SPECS["flow"]
+    path = ck.cached_checkpoint("flow", ckpt_dir)
+    B = 9
+    cond, x0 = ck.inputs(spec, batch=B)
+    o = oracle.Oracle(path, threads=0)
+    say(f"flow RK4-4 batch={B} (matrix cores)")
+    with flowedge_amd.Engine(path) as e:
+        got = e.sample_condition_batch(cond, x0, steps=4, method="rk4")
+    err = maxerr(got, o.sample_batch(cond, x0, 4, 1, flowedge_amd.SOLVERS["rk4"], workers=8))
+    say(f"flow batch={B} max err {err:.3e}")
+    assert err <= TOL
