@@ -160,20 +160,24 @@ __device__ __forceinline__ float stream_gaussian(std::uint64_t seed, std::uint64
   return (n & 1) ? radius * sinf(angle) : radius * cosf(angle);
 }
 
-constexpr int kMaxUpdateChannelsPerLane = 4;  // c0 <= 1024
+constexpr int kUpdThreads = 512;
+constexpr int kMaxUpdateChannelsPerLane = 2;  // c0 <= 1024
 constexpr int kMaxUpdateGroups = 32;
 constexpr int kMaxActions = 64;
 
-// One block per sample.  Lane l owns channels l, l+256, ...: loads them, the block reduces the
-// GroupNorm statistics, applies GN + Mish, and reduces the 1x1 conv over channels per action
-// channel (wavefront reduce-scatter over the H positions + LDS across wavefronts).  The update then
-// runs on the A*H state values.
+// One block per sample.  Lane l owns channels l and l + 512 (H positions each, loaded as 16-byte
+// vectors); the block reduces the GroupNorm statistics (fp64), applies GN + Mish, and forms the
+// 1x1 conv's partial sums for up to 64 / H actions at a time, folded by one wavefront
+// reduce-scatter and one LDS pass per action group.  The update then runs on the A*H state values.
 template <int H>
-__global__ __launch_bounds__(kBlock) void update_kernel(UpdateOp op) {
-  __shared__ double ps[kBlock * kMaxUpdateChannelsPerLane];
-  __shared__ double pq[kBlock * kMaxUpdateChannelsPerLane];
+__global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
+  constexpr int CPL = kMaxUpdateChannelsPerLane;
+  constexpr int AG = H >= kWave ? 1 : kWave / H;  // actions per reduction pass
+  constexpr int V = AG * H;
+  __shared__ double ps[kUpdThreads * CPL];
+  __shared__ double pq[kUpdThreads * CPL];
   __shared__ float gmean[kMaxUpdateGroups], ginv[kMaxUpdateGroups];
-  __shared__ float red[kBlock / kWave][H];
+  __shared__ float red[kUpdThreads / kWave][V];
   __shared__ float eps[kMaxActions][H];
   const int b = blockIdx.x;
   const int A = op.action_dim, C = op.c0;
@@ -181,14 +185,27 @@ __global__ __launch_bounds__(kBlock) void update_kernel(UpdateOp op) {
   const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
   const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
 
-  float hv[kMaxUpdateChannelsPerLane][H];
+  float hv[CPL][H];
 #pragma unroll
-  for (int i = 0; i < kMaxUpdateChannelsPerLane; ++i) {
-    const int c = tid + i * kBlock;
+  for (int i = 0; i < CPL; ++i) {
+    const int c = tid + i * kUpdThreads;
+    const float* p = hb + static_cast<std::int64_t>(c) * H;
+    if constexpr (H >= 4) {
+#pragma unroll
+      for (int t = 0; t < H; t += 4) {
+        const float4 v = c < C ? *reinterpret_cast<const float4*>(p + t) : float4{0, 0, 0, 0};
+        hv[i][t] = v.x;
+        hv[i][t + 1] = v.y;
+        hv[i][t + 2] = v.z;
+        hv[i][t + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < H; ++t) hv[i][t] = c < C ? p[t] : 0.0f;
+    }
     double s = 0.0, q = 0.0;
 #pragma unroll
     for (int t = 0; t < H; ++t) {
-      hv[i][t] = c < C ? hb[static_cast<std::int64_t>(c) * H + t] : 0.0f;
       const double d = static_cast<double>(hv[i][t]);
       s += d;
       q += d * d;
@@ -200,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void update_kernel(UpdateOp op) {
   }
   __syncthreads();
   const int cpg = C / op.groups;
-  for (int g = wave; g < op.groups; g += kBlock / kWave) {
+  for (int g = wave; g < op.groups; g += kUpdThreads / kWave) {
     double s = 0.0, q = 0.0;
     for (int i = lane; i < cpg; i += kWave) {
       s += ps[g * cpg + i];
@@ -218,45 +235,48 @@ __global__ __launch_bounds__(kBlock) void update_kernel(UpdateOp op) {
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kMaxUpdateChannelsPerLane; ++i) {
-    const int c = tid + i * kBlock;
+  for (int i = 0; i < CPL; ++i) {
+    const int c = tid + i * kUpdThreads;
     if (c < C) {
       const int g = c / cpg;
       const float scale = ginv[g] * op.gamma[c];
+      const float shift = op.beta[c];
+      const float mean = gmean[g];
 #pragma unroll
-      for (int t = 0; t < H; ++t) hv[i][t] = mish_f(fmaf(hv[i][t] - gmean[g], scale, op.beta[c]));
+      for (int t = 0; t < H; ++t) hv[i][t] = mish_fast(fmaf(hv[i][t] - mean, scale, shift));
     }
   }
-  for (int a = 0; a < A; ++a) {
-    float p[H];
+  for (int a0 = 0; a0 < A; a0 += AG) {
+    float p[V];
 #pragma unroll
-    for (int t = 0; t < H; ++t) p[t] = 0.0f;
+    for (int v = 0; v < V; ++v) p[v] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMaxUpdateChannelsPerLane; ++i) {
-      const int c = tid + i * kBlock;
+    for (int i = 0; i < CPL; ++i) {
+      const int c = tid + i * kUpdThreads;
       if (c < C) {
-        const float w = op.wo[static_cast<std::int64_t>(a) * C + c];
 #pragma unroll
-        for (int t = 0; t < H; ++t) p[t] = fmaf(w, hv[i][t], p[t]);
+        for (int aa = 0; aa < AG; ++aa) {
+          const int a = a0 + aa;
+          const float w = a < A ? op.wo[static_cast<std::int64_t>(a) * C + c] : 0.0f;
+#pragma unroll
+          for (int t = 0; t < H; ++t) p[aa * H + t] = fmaf(w, hv[i][t], p[aa * H + t]);
+        }
       }
     }
-    rs_step<H, 32>(p, lane);
-    constexpr int NF = H >= kWave ? H / kWave : 1;
-    const int off = rs_offset<H>(lane);
-    if (rs_writer<H>(lane)) {
-#pragma unroll
-      for (int i = 0; i < NF; ++i) red[wave][off + i] = p[i];
-    }
+    rs_step<V, 32>(p, lane);
+    const int off = rs_offset<V>(lane);
+    if (rs_writer<V>(lane)) red[wave][off] = p[0];
     __syncthreads();
-    if (tid < H) {
+    if (tid < V) {
       float s = 0.0f;
-      for (int w = 0; w < kBlock / kWave; ++w) s += red[w][tid];
-      eps[a][tid] = s + op.bo[a];
+      for (int w = 0; w < kUpdThreads / kWave; ++w) s += red[w][tid];
+      const int a = a0 + tid / H;
+      if (a < A) eps[a][tid % H] = s + op.bo[a];
     }
     __syncthreads();
   }
 
-  for (int i = tid; i < A * H; i += kBlock) {
+  for (int i = tid; i < A * H; i += kUpdThreads) {
     const int a = i / H, t = i % H;  // state layout [A][H]
     const float e = eps[a][t];
     const std::int64_t si = sample + i;
@@ -354,7 +374,7 @@ hipError_t begin_sample(const float* noise, float* x, float* xin, int batch, int
 }
 
 bool update_supported(int c0, int groups, int horizon, int action_dim) {
-  return c0 > 0 && c0 <= kBlock * kMaxUpdateChannelsPerLane && groups > 0 &&
+  return c0 > 0 && c0 <= kUpdThreads * kMaxUpdateChannelsPerLane && groups > 0 &&
          groups <= kMaxUpdateGroups && c0 % groups == 0 && action_dim > 0 &&
          action_dim <= kMaxActions &&
          (horizon == 1 || horizon == 2 || horizon == 4 || horizon == 8 || horizon == 16);
@@ -363,11 +383,11 @@ bool update_supported(int c0, int groups, int horizon, int action_dim) {
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream) {
   if (!update_supported(op.c0, op.groups, op.horizon, op.action_dim)) return hipErrorInvalidValue;
   switch (op.horizon) {
-    case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(kBlock), 0, stream, op); break;
-    case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(kBlock), 0, stream, op); break;
-    case 4: hipLaunchKernelGGL(update_kernel<4>, dim3(batch), dim3(kBlock), 0, stream, op); break;
-    case 8: hipLaunchKernelGGL(update_kernel<8>, dim3(batch), dim3(kBlock), 0, stream, op); break;
-    default: hipLaunchKernelGGL(update_kernel<16>, dim3(batch), dim3(kBlock), 0, stream, op); break;
+    case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
+    case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
+    case 4: hipLaunchKernelGGL(update_kernel<4>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
+    case 8: hipLaunchKernelGGL(update_kernel<8>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
+    default: hipLaunchKernelGGL(update_kernel<16>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
   }
   return hipGetLastError();
 }
