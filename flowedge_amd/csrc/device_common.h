@@ -77,10 +77,32 @@ __device__ __forceinline__ bool rs_writer(int lane) {
   }
 }
 
+// v + (v of lane l ^ 1), (l ^ 2), rotations by 4 and 8 within each 16-lane row, through DPP
+// moves of the two 32-bit halves (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ double dpp_add(double v) {
+  const long long bits = __builtin_bit_cast(long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(bits), CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(bits >> 32), CTRL, 0xf, 0xf, false);
+  const long long moved = (static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo);
+  return v + __builtin_bit_cast(double, moved);
+}
+
+__device__ __forceinline__ double lane_value(double v, int lane) {
+  const long long bits = __builtin_bit_cast(long long, v);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
+  return __builtin_bit_cast(double, (static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
+}
+
+// Sum over the 64 lanes of a wavefront, returned to every lane: each 16-lane row is reduced with
+// DPP (quad_perm xor 1, xor 2, row_ror 4, row_ror 8), then the four row sums are read out.
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  v = dpp_add<0xb1>(v);
+  v = dpp_add<0x4e>(v);
+  v = dpp_add<0x124>(v);
+  v = dpp_add<0x128>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 }  // namespace fe::hip::dev
