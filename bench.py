@@ -92,21 +92,36 @@ def shape_of(name: str) -> str:
     return name[name.index("["):] if "[" in name else name
 
 
-def conv_breakdown(eng, iters: int = 50):
+def conv_flops(shape: str) -> int:
+    """FLOPs of one sample through a convolution named "[oc<-ic Kk Llin (down|up)? ... (+1x1)?]"."""
+    f = shape.strip("[]").split()
+    oc, ic = (int(v) for v in f[0].split("<-"))
+    k, lin = int(f[1][1:]), int(f[2][1:])
+    lout = lin // 2 if "down" in f else (2 * lin if "up" in f else lin)
+    flops = 2 * oc * ic * k * (lin if "up" in f else lout)  # ConvT: 2*OC*IC*K*L_in
+    if "+1x1" in f:
+        flops += 2 * oc * ic * lout
+    return flops
+
+
+def conv_breakdown(eng, batch: int = 1, iters: int = 50):
     """Mean launch time of every convolution shape of one U-Net evaluation (each shape's distinct
-    layers launched round-robin) and its share of an evaluation."""
+    layers launched round-robin, on the kernels a call of this batch uses) and its share of an
+    evaluation."""
     convs = eng.convolutions()
     groups = {}
     for c in convs:
         groups.setdefault(shape_of(c["name"]), []).append(c)
     rows = []
     for shape, cs in groups.items():
-        us = eng.time_convolutions([c["index"] for c in cs], batch=1, iters=iters)
-        nbytes = cs[0]["weight_bytes"] + cs[0]["sample_bytes"]
-        rows.append({"shape": shape, "launches_per_nfe": len(cs), "us_per_launch": round(us, 3),
-                     "us_per_nfe": round(us * len(cs), 2), "bytes_per_launch": nbytes,
-                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                     "indices": [c["index"] for c in cs]})
+        us = eng.time_convolutions([c["index"] for c in cs], batch=batch, iters=iters)
+        nbytes = cs[0]["weight_bytes"] + cs[0]["sample_bytes"] * batch
+        row = {"shape": shape, "launches_per_nfe": len(cs), "us_per_launch": round(us, 3),
+               "us_per_nfe": round(us * len(cs), 2), "bytes_per_launch": nbytes,
+               "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "indices": [c["index"] for c in cs]}
+        if batch > 1:
+            row["tflops"] = round(conv_flops(shape) * batch / (us * 1e-6) / 1e12, 2)
+        rows.append(row)
     rows.sort(key=lambda r: -r["us_per_nfe"])
     return rows
 
@@ -294,8 +309,14 @@ def main():
         }
         large["frac_of_fp32_mfma_peak"] = large["tflops"] / FP32_MFMA_PEAK_TFLOPS
         print(f"[bench] B={B} DDIM-10 tick p50 {bp50:.2f} ms", file=sys.stderr, flush=True)
+        bd_large = conv_breakdown(eng, batch=B, iters=5)
+        for r in bd_large:
+            print(f"[bench] B={B} {r['shape']:34s} x{r['launches_per_nfe']}  {r['us_per_launch']:9.1f} us"
+                  f"  {r.get('tflops', 0):6.1f} TFLOP/s  {r['us_per_nfe']:9.1f} us/NFE",
+                  file=sys.stderr, flush=True)
+        large["conv_breakdown"] = [{k: v for k, v in r.items() if k != "indices"} for r in bd_large]
 
-    breakdown = conv_breakdown(eng)
+    breakdown = conv_breakdown(eng, batch=1)
     for r in breakdown:
         print(f"[bench] {r['shape']:34s} x{r['launches_per_nfe']}  {r['us_per_launch']:8.2f} us"
               f"  {r['gbs']:7.1f} GB/s  {r['us_per_nfe']:8.1f} us/NFE", file=sys.stderr, flush=True)

@@ -6,10 +6,11 @@
 // Mish (+ FiLM) (+ residual) prologue runs first as its own per-sample kernel (norm_act), whose
 // output the GEMM reads as a plain tensor.
 //
-// GEMM tiling: a 256-lane workgroup owns MT output channels x 128 columns (samples x output
-// positions); its four wavefronts each own (MT/2) x 64.  The K loop walks 16 input channels at a
-// time (all taps), double-buffered in LDS: the next step's weights and inputs are loaded into
-// registers while the matrix cores work on the current one.  Within a 16-channel step a lane
+// GEMM tiling: a 256-lane workgroup owns 64 output channels x NT columns (samples x output
+// positions, NT = 128, or 64 when 128 would leave CUs without a workgroup); its four wavefronts
+// each own 32 x (NT/2).  The K loop walks 16 input channels at a time (all taps), double-buffered
+// in LDS: the next step's weights and inputs are loaded into registers while the matrix cores
+// work on the current one.  Within a 16-channel step a lane
 // feeds the MFMA k-slot (lane / 16) with channels 4 * (lane / 16) + s over four MFMAs s, so
 // every operand read is one 16-byte LDS load.  Output positions whose input index falls in the
 // padding read a zero row.  Workgroups that share a weight tile are placed on the same XCD
@@ -33,7 +34,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMmThreads = 256;
 constexpr int kKC = 16;   // input channels per K step
-constexpr int kNT = 128;  // columns per workgroup
 constexpr int kPad = 4;   // LDS row padding (floats)
 
 __host__ __device__ constexpr int lout_for(int mode, int lin) {
@@ -71,10 +71,10 @@ __device__ __forceinline__ int src_at(int t, int k) {
   }
 }
 
-template <int MODE, int K, int LIN, int MT>
+template <int MODE, int K, int LIN, int MT, int NT>
 struct MmShape {
   static constexpr int LOUT = lout_for(MODE, LIN);
-  static constexpr int SB = kNT / LOUT;          // samples per column tile
+  static constexpr int SB = NT / LOUT;           // samples per column tile
   static constexpr int WROW = K * kKC + kPad;    // LDS floats per weight row
   static constexpr int XROW = kKC + kPad;        // LDS floats per (sample, position) row
   static constexpr int ZERO = SB * LIN;          // index of the zero row
@@ -84,11 +84,12 @@ struct MmShape {
   static constexpr int UW = MT * K * 4 / kMmThreads;  // weight float4 per lane per step
   static constexpr int XELEMS = SB * kKC * LIN;       // input floats per step
   static constexpr int XV = LIN >= 4 ? 4 : 1;          // vector width of input loads
-  static constexpr int UX = XELEMS / XV / kMmThreads;
-  static constexpr int WM = MT / 2, WN = kNT / 2;
+  static constexpr int XUNITS = XELEMS / XV;
+  static constexpr int UX = (XUNITS + kMmThreads - 1) / kMmThreads;
+  static constexpr int WM = MT / 2, WN = NT / 2;
   static constexpr int TI = WM / 16, TJ = WN / 16;
   static_assert(MT * K * 4 % kMmThreads == 0, "weight units per lane");
-  static_assert(XELEMS % (XV * kMmThreads) == 0, "input units per lane");
+  static_assert(NT % LOUT == 0 && XELEMS % XV == 0, "column tile");
 };
 
 template <bool BF16>
@@ -102,9 +103,9 @@ __device__ __forceinline__ float4 load_w4(const void* base, std::int64_t idx) {
   }
 }
 
-template <int MODE, int K, int LIN, bool BF16, int MT>
+template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
 __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
-  using S = MmShape<MODE, K, LIN, MT>;
+  using S = MmShape<MODE, K, LIN, MT, NT>;
   extern __shared__ float4 lds4[];
   float* Ws = reinterpret_cast<float*>(lds4);  // [2][WFLOATS]
   float* Xs = Ws + 2 * S::WFLOATS;             // [2][XFLOATS]
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   const int mt = id / a.ntiles, nt = id - mt * a.ntiles;
   const int m0 = mt * MT;
   const int b0 = nt * S::SB;
-  const int nsteps = a.ic / kKC;
+  const int nsteps = (a.ic + kKC - 1) / kKC;
 
   // Zero rows of both input buffers (never overwritten).
   if (tid < 2 * kKC) Xs[(tid / kKC) * S::XFLOATS + S::ZERO * S::XROW + (tid % kKC)] = 0.0f;
@@ -134,8 +135,24 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
       const int m = u / (K * 4), rem = u - m * (K * 4);
       const int k = rem >> 2, q = rem & 3;
       const int oc = m0 + m;
-      wreg[r] = oc < a.oc ? load_w4<BF16>(a.w, (static_cast<std::int64_t>(oc) * K + k) * a.ic + ic0 + 4 * q)
-                          : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (NARROW) {
+        // Channel counts that are not a multiple of 16: element-wise guarded loads.
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = ic0 + 4 * q + e;
+          const std::int64_t idx = (static_cast<std::int64_t>(oc) * K + k) * a.ic + c;
+          v[e] = 0.0f;
+          if (oc < a.oc && c < a.ic)
+            v[e] = BF16 ? __uint_as_float(static_cast<unsigned>(
+                              static_cast<const unsigned short*>(a.w)[idx]) << 16)
+                        : static_cast<const float*>(a.w)[idx];
+        }
+        wreg[r] = float4{v[0], v[1], v[2], v[3]};
+      } else {
+        wreg[r] = oc < a.oc ? load_w4<BF16>(a.w, (static_cast<std::int64_t>(oc) * K + k) * a.ic + ic0 + 4 * q)
+                            : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
 #pragma unroll
     for (int r = 0; r < S::UX; ++r) {
@@ -145,7 +162,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
         const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
         const int b = b0 + bl, c = ic0 + ch;
         float4 val = float4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (b < a.batch) {
+        if (u < S::XUNITS && b < a.batch && (!NARROW || c < a.ic)) {
           const float* p = c < a.split ? a.src + b * a.src_stride + static_cast<std::int64_t>(c) * LIN
                                        : a.plain + b * a.plain_stride +
                                              static_cast<std::int64_t>(c - a.split) * LIN;
@@ -157,7 +174,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
         const int ch = v / LIN, t = v - ch * LIN;
         const int b = b0 + bl, c = ic0 + ch;
         float val = 0.0f;
-        if (b < a.batch)
+        if (u < S::XUNITS && b < a.batch && (!NARROW || c < a.ic))
           val = c < a.split ? a.src[b * a.src_stride + static_cast<std::int64_t>(c) * LIN + t]
                             : a.plain[b * a.plain_stride + static_cast<std::int64_t>(c - a.split) * LIN + t];
         xs1[r] = val;
@@ -177,6 +194,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
 #pragma unroll
     for (int r = 0; r < S::UX; ++r) {
       const int u = tid + r * kMmThreads;
+      if (u >= S::XUNITS) continue;
       if constexpr (S::XV == 4) {
         const int bl = u / (4 * LIN), v = u - bl * (4 * LIN);
         const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
@@ -341,11 +359,15 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
   }
 }
 
-template <int MODE, int K, int LIN, bool BF16, int MT>
+// Tile configurations: 64 output channels x 128 columns, or 64 x 64 when the larger column tile
+// would leave CUs without a workgroup.
+enum MmTile : int { kTile64x128 = 0, kTile64x64 = 1 };
+
+template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
 hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
-  using S = MmShape<MODE, K, LIN, MT>;
+  using S = MmShape<MODE, K, LIN, MT, NT>;
   const std::size_t smem = (2 * S::WFLOATS + 2 * S::XFLOATS) * sizeof(float);
-  auto fn = conv_mfma_kernel<MODE, K, LIN, BF16, MT>;
+  auto fn = conv_mfma_kernel<MODE, K, LIN, BF16, MT, NT, NARROW>;
   static bool raised = false;
   if (!raised && smem > 48 * 1024) {
     const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -359,21 +381,26 @@ hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
 }
 
 template <int MODE, int K, int LIN, bool BF16>
-hipError_t by_mt(int mt, const MmArgs& a, hipStream_t s) {
-  return mt == 128 ? launch_mm<MODE, K, LIN, BF16, 128>(a, s) : launch_mm<MODE, K, LIN, BF16, 64>(a, s);
+hipError_t by_tile(int tile, bool narrow, const MmArgs& a, hipStream_t s) {
+  if (narrow) {
+    if constexpr (MODE == kConvSame) return launch_mm<MODE, K, LIN, BF16, 64, 64, true>(a, s);
+    return hipErrorInvalidValue;
+  }
+  return tile == kTile64x128 ? launch_mm<MODE, K, LIN, BF16, 64, 128, false>(a, s)
+                             : launch_mm<MODE, K, LIN, BF16, 64, 64, false>(a, s);
 }
 
 template <int MODE, int K, bool BF16>
-hipError_t by_lin_mm(int lin, int mt, const MmArgs& a, hipStream_t s) {
+hipError_t by_lin_mm(int lin, int tile, bool narrow, const MmArgs& a, hipStream_t s) {
   switch (lin) {
     case 1:
-      if constexpr (MODE != kConvDown) return by_mt<MODE, K, 1, BF16>(mt, a, s);
+      if constexpr (MODE != kConvDown) return by_tile<MODE, K, 1, BF16>(tile, narrow, a, s);
       break;
-    case 2: return by_mt<MODE, K, 2, BF16>(mt, a, s);
-    case 4: return by_mt<MODE, K, 4, BF16>(mt, a, s);
-    case 8: return by_mt<MODE, K, 8, BF16>(mt, a, s);
+    case 2: return by_tile<MODE, K, 2, BF16>(tile, narrow, a, s);
+    case 4: return by_tile<MODE, K, 4, BF16>(tile, narrow, a, s);
+    case 8: return by_tile<MODE, K, 8, BF16>(tile, narrow, a, s);
     case 16:
-      if constexpr (MODE != kConvTranspose) return by_mt<MODE, K, 16, BF16>(mt, a, s);
+      if constexpr (MODE != kConvTranspose) return by_tile<MODE, K, 16, BF16>(tile, narrow, a, s);
       break;
     default: break;
   }
@@ -381,18 +408,18 @@ hipError_t by_lin_mm(int lin, int mt, const MmArgs& a, hipStream_t s) {
 }
 
 template <bool BF16>
-hipError_t by_kernel_mm(const ConvOp& op, int mt, const MmArgs& a, hipStream_t s) {
+hipError_t by_kernel_mm(const ConvOp& op, int tile, bool narrow, const MmArgs& a, hipStream_t s) {
   if (op.mode == kConvSame) {
     switch (op.k) {
-      case 1: return by_lin_mm<kConvSame, 1, BF16>(op.lin, mt, a, s);
-      case 3: return by_lin_mm<kConvSame, 3, BF16>(op.lin, mt, a, s);
-      case 5: return by_lin_mm<kConvSame, 5, BF16>(op.lin, mt, a, s);
+      case 1: return by_lin_mm<kConvSame, 1, BF16>(op.lin, tile, narrow, a, s);
+      case 3: return by_lin_mm<kConvSame, 3, BF16>(op.lin, tile, narrow, a, s);
+      case 5: return by_lin_mm<kConvSame, 5, BF16>(op.lin, tile, narrow, a, s);
       default: return hipErrorInvalidValue;
     }
   }
-  if (op.mode == kConvDown && op.k == 3) return by_lin_mm<kConvDown, 3, BF16>(op.lin, mt, a, s);
+  if (op.mode == kConvDown && op.k == 3) return by_lin_mm<kConvDown, 3, BF16>(op.lin, tile, narrow, a, s);
   if (op.mode == kConvTranspose && op.k == 4)
-    return by_lin_mm<kConvTranspose, 4, BF16>(op.lin, mt, a, s);
+    return by_lin_mm<kConvTranspose, 4, BF16>(op.lin, tile, narrow, a, s);
   return hipErrorInvalidValue;
 }
 
@@ -407,7 +434,12 @@ bool lin_mm_ok(int mode, int lin) {
 
 bool conv_mfma_supported(const ConvOp& op, int split) {
   if (!lin_mm_ok(op.mode, op.lin) || op.lout != lout_for(op.mode, op.lin)) return false;
-  if (op.ic % kKC != 0 || split % kKC != 0 || split > op.ic || op.oc <= 0) return false;
+  if (split > op.ic || split <= 0 || op.oc <= 0 || op.ic <= 0) return false;
+  if (op.ic % kKC != 0) {
+    // Narrow inputs (the first convolution reads action_dim channels): one plain source.
+    return split == op.ic && op.mode == kConvSame && (op.k == 1 || op.k == 3 || op.k == 5);
+  }
+  if (split % kKC != 0) return false;
   if (op.mode == kConvSame) return op.k == 1 || op.k == 3 || op.k == 5;
   if (op.mode == kConvDown) return op.k == 3;
   return op.mode == kConvTranspose && op.k == 4;
@@ -431,13 +463,16 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   a.oc = op.oc;
   a.ic = op.ic;
   a.batch = batch;
-  const int sb = kNT / op.lout;
-  a.ntiles = (batch + sb - 1) / sb;
-  // 128-row tiles when they alone give every CU a workgroup, else 64-row tiles.
-  int mt = 128;
-  if (((op.oc + 127) / 128) * a.ntiles < 256) mt = 64;
-  a.mtiles = (op.oc + mt - 1) / mt;
-  return op.bf16 ? by_kernel_mm<true>(op, mt, a, stream) : by_kernel_mm<false>(op, mt, a, stream);
+  const bool narrow = op.ic % kKC != 0;
+  a.mtiles = (op.oc + 63) / 64;
+  int tile = kTile64x128;
+  a.ntiles = (batch + 128 / op.lout - 1) / (128 / op.lout);
+  if (narrow || a.mtiles * a.ntiles < 256) {
+    tile = kTile64x64;
+    a.ntiles = (batch + 64 / op.lout - 1) / (64 / op.lout);
+  }
+  return op.bf16 ? by_kernel_mm<true>(op, tile, narrow, a, stream)
+                 : by_kernel_mm<false>(op, tile, narrow, a, stream);
 }
 
 hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,

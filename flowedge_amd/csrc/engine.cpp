@@ -633,6 +633,10 @@ void bind_all(FeEngine& e) {
     if (fe_st_ != hipSuccess) return fe_st_; \
   } while (0)
 
+hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
+                         const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
+                         int batch, hipStream_t s);
+
 // Launches one fused convolution; while recording, also keeps its arguments and algorithmic
 // bytes (each weight and bias once, each activation and per-channel parameter once per sample).
 hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
@@ -670,6 +674,13 @@ hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
     r.sample_bytes = sb;
     e.conv_records.push_back(std::move(r));
   }
+  return dispatch_conv(e, op, res, in, y, yr, batch, s);
+}
+
+// Runs one fused convolution on the kernels chosen for this batch size.
+hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
+                         const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
+                         int batch, hipStream_t s) {
   using namespace fe::hip;
   if (static_cast<std::size_t>(batch) >= e.mfma_batch && conv_mfma_supported(op, in.split) &&
       (res == nullptr || conv_mfma_supported(*res, in.split))) {
@@ -1691,8 +1702,8 @@ int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, siz
   auto round = [&]() -> hipError_t {
     for (size_t i = 0; i < n; ++i) {
       const FeEngine::ConvRecord& r = e->conv_records[indices[i]];
-      const hipError_t s2 = fe::hip::conv_fused(r.op, r.has_res ? &r.res : nullptr, r.in, r.y,
-                                                r.yr, b, e->stream);
+      const hipError_t s2 = dispatch_conv(*e, r.op, r.has_res ? &r.res : nullptr, r.in, r.y,
+                                          r.yr, b, e->stream);
       if (s2 != hipSuccess) return s2;
     }
     return hipSuccess;

@@ -223,9 +223,10 @@ int fe_engine_conv_count(fe_engine* engine, size_t* count);
 int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name_capacity,
                         uint64_t* weight_bytes, uint64_t* sample_bytes);
 
-/* Launches convolutions indices[0..n) round-robin `iters` times at `batch` on the engine's stream
- * and returns the mean device time of one launch in microseconds (hipEvents around the loop, after
- * one untimed round).  Outputs land in the engine's own buffers. */
+/* Launches convolutions indices[0..n) round-robin `iters` times at `batch` on the engine's stream,
+ * on the kernels a sampling call of that batch uses, and returns the mean device time of one
+ * launch in microseconds (hipEvents around the loop, after one untimed round).  Outputs land in
+ * the engine's own buffers. */
 int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, size_t batch,
                          size_t iters, float* avg_us);
 
