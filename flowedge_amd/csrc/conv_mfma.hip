@@ -52,6 +52,8 @@ struct MmArgs {
   std::int64_t plain_stride;
   int oc, ic, batch;
   int mtiles, ntiles;
+  int ksplit;   // workgroups sharing one output tile's K range (1: no split)
+  float* part;  // ksplit > 1: partial tiles [ksplit][mtiles * ntiles][64 * NT]
 };
 
 // Input index read by output t through tap k, or -1 in the padding (t known only at run time).
@@ -112,14 +114,19 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // Tile index, grouped so that the workgroups on one XCD share weight tiles.
+  // Tile index, grouped so that the workgroups on one XCD share weight tiles; with a split K
+  // loop, workgroup (ks, tile) covers K steps [ks * n / ksplit, (ks + 1) * n / ksplit).
   int id = blockIdx.x;
-  const int total = a.mtiles * a.ntiles;
+  const int tiles = a.mtiles * a.ntiles;
+  const int total = tiles * a.ksplit;
   if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
-  const int mt = id / a.ntiles, nt = id - mt * a.ntiles;
+  const int ks = id / tiles;
+  const int tile = id - ks * tiles;
+  const int mt = tile / a.ntiles, nt = tile - mt * a.ntiles;
   const int m0 = mt * MT;
   const int b0 = nt * S::SB;
-  const int nsteps = (a.ic + kKC - 1) / kKC;
+  const int nall = (a.ic + kKC - 1) / kKC;
+  const int s0 = ks * nall / a.ksplit, s1 = (ks + 1) * nall / a.ksplit;
 
   // Zero rows of both input buffers (never overwritten).
   if (tid < 2 * kKC) Xs[(tid / kKC) * S::XFLOATS + S::ZERO * S::XROW + (tid % kKC)] = 0.0f;
@@ -233,12 +240,12 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
 #pragma unroll
     for (int j = 0; j < S::TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  load_step(0);
+  load_step(s0);
   store_step(0);
   __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    if (step + 1 < nsteps) load_step(step + 1);
+  for (int step = s0; step < s1; ++step) {
+    const int buf = (step - s0) & 1;
+    if (step + 1 < s1) load_step(step + 1);
     const float* W = Ws + buf * S::WFLOATS;
     const float* X = Xs + buf * S::XFLOATS;
 #pragma unroll
@@ -259,11 +266,22 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
         }
     }
-    if (step + 1 < nsteps) store_step(buf ^ 1);
+    if (step + 1 < s1) store_step(buf ^ 1);
     __syncthreads();
   }
 
   // Epilogue: lane holds rows 4 * (lane / 16) + e of each 16x16 tile, column lane % 16.
+  if (a.ksplit > 1) {
+    float* P = a.part + (static_cast<std::int64_t>(ks) * tiles + tile) * (MT * NT);
+#pragma unroll
+    for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < S::TJ; ++j)
+          P[(wr * S::WM + 16 * i + 4 * kq + e) * NT + wc * S::WN + 16 * j + l16] = acc[i][j][e];
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < S::TI; ++i)
 #pragma unroll
@@ -280,6 +298,24 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
           a.y[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] = acc[i][j][e] + bias;
       }
     }
+}
+
+// Sums the ksplit partial tiles of a split-K convolution in a fixed order and adds the bias.
+__global__ __launch_bounds__(kMmThreads) void splitk_reduce_kernel(MmArgs a, int nt_cols, int lout) {
+  const int tiles = a.mtiles * a.ntiles;
+  const int per = 64 * nt_cols;
+  const std::int64_t e = static_cast<std::int64_t>(blockIdx.x) * kMmThreads + threadIdx.x;
+  if (e >= static_cast<std::int64_t>(tiles) * per) return;
+  const int tile = static_cast<int>(e / per), local = static_cast<int>(e - static_cast<std::int64_t>(tile) * per);
+  float sum = 0.0f;
+  for (int ks = 0; ks < a.ksplit; ++ks)
+    sum += a.part[(static_cast<std::int64_t>(ks) * tiles + tile) * per + local];
+  const int mt = tile / a.ntiles, nt = tile - mt * a.ntiles;
+  const int r = local / nt_cols, c = local - r * nt_cols;
+  const int oc = mt * 64 + r;
+  const int b = nt * (nt_cols / lout) + c / lout, t = c % lout;
+  if (oc < a.oc && b < a.batch)
+    a.y[b * a.ys + static_cast<std::int64_t>(oc) * lout + t] = sum + a.bias[oc];
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -376,7 +412,7 @@ hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
     if (st != hipSuccess) return st;
     raised = true;
   }
-  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles), dim3(kMmThreads), smem, s, a);
+  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles * a.ksplit), dim3(kMmThreads), smem, s, a);
   return hipGetLastError();
 }
 
@@ -447,7 +483,7 @@ bool conv_mfma_supported(const ConvOp& op, int split) {
 
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
-                     hipStream_t stream) {
+                     float* workspace, std::size_t workspace_floats, hipStream_t stream) {
   if (!conv_mfma_supported(op, split) || batch <= 0) return hipErrorInvalidValue;
   if (split < op.ic && plain == nullptr) return hipErrorInvalidValue;
   MmArgs a{};
@@ -471,8 +507,28 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
     tile = kTile64x64;
     a.ntiles = (batch + 64 / op.lout - 1) / (64 / op.lout);
   }
-  return op.bf16 ? by_kernel_mm<true>(op, tile, narrow, a, stream)
-                 : by_kernel_mm<false>(op, tile, narrow, a, stream);
+  // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
+  // workgroups per CU, so that two K steps of weights stream per CU at a time.
+  const int nt_cols = tile == kTile64x128 ? 128 : 64;
+  const int tiles = a.mtiles * a.ntiles;
+  const int nsteps = (op.ic + kKC - 1) / kKC;
+  a.ksplit = 1;
+  if (tiles < 256 && workspace != nullptr) {
+    int ks = (512 + tiles - 1) / tiles;
+    if (ks > nsteps) ks = nsteps;
+    const std::size_t need = static_cast<std::size_t>(ks) * tiles * 64 * nt_cols;
+    if (ks > 1 && need <= workspace_floats) {
+      a.ksplit = ks;
+      a.part = workspace;
+    }
+  }
+  const hipError_t st = op.bf16 ? by_kernel_mm<true>(op, tile, narrow, a, stream)
+                                : by_kernel_mm<false>(op, tile, narrow, a, stream);
+  if (st != hipSuccess || a.ksplit == 1) return st;
+  const std::int64_t elems = static_cast<std::int64_t>(tiles) * 64 * nt_cols;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((elems + kMmThreads - 1) / kMmThreads)),
+                     dim3(kMmThreads), 0, stream, a, nt_cols, op.lout);
+  return hipGetLastError();
 }
 
 hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,

@@ -54,6 +54,7 @@ bool env_flag(const char* name) {
 constexpr unsigned kMaxPoolThreads = 8;  // engine_runtime.h:39
 constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
 constexpr std::size_t kMaxNormFloats = 8192;  // width * length of any normalised activation
+constexpr std::size_t kSplitKFloats = 1024 * 64 * 128;  // split-K partials: <= 1024 tiles of 64 x 128
 constexpr std::size_t kFinalNormGroups = 8;  // diffusion.cc:28
 constexpr std::size_t kAlign = 256;
 
@@ -252,7 +253,8 @@ struct FeEngine {
   std::size_t in_cond = 0, in_noise = 0, out_action = 0, seed_dev = 0;
   std::size_t final_in = 0;
   std::size_t xnorm = 0;       // batched path: normalised input of one convolution [B][8192]
-  std::size_t mfma_batch = 8;  // batches of at least this many samples use the matrix cores
+  std::size_t splitk = 0;      // batched path: split-K partial tiles (kSplitKFloats)
+  std::size_t mfma_batch = 4;  // batches of at least this many samples use the matrix cores
 
   std::list<GraphEntry> graphs;  // most recently used first
 
@@ -473,6 +475,7 @@ struct Builder {
     e.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
     e.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
     e.xnorm = plan.take(B * kMaxNormFloats * 4);
+    e.splitk = plan.take(kSplitKFloats * 4);
     return true;
   }
 };
@@ -695,9 +698,12 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
       src = dst;
       ss = ds;
     }
-    FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, s));
+    float* ws = e.ptr(e.splitk);
+    FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws,
+                     kSplitKFloats, s));
     if (res != nullptr)
-      FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, s));
+      FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws,
+                       kSplitKFloats, s));
     return hipSuccess;
   }
   return conv_fused(op, res, in, y, yr, batch, s);
@@ -1217,14 +1223,16 @@ int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, st
   return FE_STATUS_OK;
 }
 
-// Smallest batch that runs the convolutions on the matrix cores (FLOWEDGE_MFMA_BATCH, default 8;
-// a value above the max batch keeps every batch on the weight-streaming kernels).
+// Smallest batch that runs the convolutions on the matrix cores (FLOWEDGE_MFMA_BATCH; 0 = by
+// weight type: 4 samples for F32 convolutions, 6 for BF16, where streaming half the bytes keeps
+// the batch-1 kernels ahead longer; a value above the max batch keeps every batch on the
+// weight-streaming kernels).
 std::size_t env_mfma_batch() {
   const char* v = std::getenv("FLOWEDGE_MFMA_BATCH");
-  if (v == nullptr || *v == '\0') return 8;
+  if (v == nullptr || *v == '\0') return 0;
   char* end = nullptr;
   const unsigned long n = std::strtoul(v, &end, 10);
-  return (end && *end == '\0' && n > 0) ? n : 8;
+  return (end && *end == '\0') ? n : 0;
 }
 
 std::size_t env_max_batch() {
@@ -1275,6 +1283,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     return nullptr;
   }
   e->arena_bytes = builder.plan.size;
+  if (e->mfma_batch == 0) e->mfma_batch = e->bf16_convs ? 6 : 4;
 
   int count = 0;
   hipError_t st = hipGetDeviceCount(&count);

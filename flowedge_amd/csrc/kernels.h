@@ -76,11 +76,14 @@ hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& i
 bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm);
 
 // Batched path (matrix cores).  y = conv(x) + bias with x a plain tensor: channels [0, split)
-// from `src`, the rest from `plain`.  Needs ic and split to be multiples of 16.
+// from `src`, the rest from `plain`.  ic and split are multiples of 16, or split == ic (narrow
+// first convolution).  When the output tiles would leave CUs idle, the K loop is split over
+// workgroups whose partial tiles go to `workspace` (workspace_floats large enough) and are summed
+// by a second kernel in a fixed order.
 bool conv_mfma_supported(const ConvOp& op, int split);
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
-                     hipStream_t stream);
+                     float* workspace, std::size_t workspace_floats, hipStream_t stream);
 
 // The prologue of a ConvInput with `norm` on its own: dst[b][0 : split*lin) =
 // mish(GN(src)) [* scale + shift] [+ res], per sample.
