@@ -156,6 +156,61 @@ def dominant_roofline(eng, iters: int):
     }
 
 
+EXTRA_CONFIGS = [
+    # (workload, batch, kind 0 = DDIM / 1 = flow ODE, steps, mode, U-Net evaluations per step, label)
+    ("bimanual", 1, 0, 10, 0, 1, "4a: bimanual-size BF16 (H8, A14, cond 1052), B=1, DDIM-10"),
+    ("bimanual", 64, 0, 10, 0, 1, "4b: bimanual-size BF16, B=64, DDIM-10"),
+    ("flow", 1, 1, 4, 2, 4, "5: flow U-Net (A7, cond 256), B=1, RK4-4"),
+    ("flow", 1, 1, 10, 0, 1, "5: flow U-Net, B=1, Euler-10"),
+    ("flow", 128, 1, 4, 2, 4, "5b: flow U-Net, B=128, RK4-4"),
+    ("flow", 128, 1, 10, 0, 1, "5b: flow U-Net, B=128, Euler-10"),
+]
+
+
+def extra_configs(iters: int = 10):
+    """Device time of the other configurations of the path (one graph replay each)."""
+    import numpy as np
+    import torch
+
+    import flowedge_amd
+    from flowedge_amd import checkpoint as ck
+
+    dev = torch.device("cuda:0")
+    engines = {}
+    rows = []
+    for work, batch, kind, steps, mode, per_step, label in EXTRA_CONFIGS:
+        spec = ck.SPECS[work]
+        if work not in engines:
+            engines[work] = flowedge_amd.Engine(ck.cached_checkpoint(work))
+        e = engines[work]
+        cond, noise = ck.inputs(spec, batch=batch)
+        dc, dn = torch.from_numpy(cond).to(dev), torch.from_numpy(noise).to(dev)
+        do = torch.empty((batch, spec.horizon, spec.action_dim), dtype=torch.float32, device=dev)
+        e.prepare(kind, batch, steps, mode)
+        for _ in range(3):
+            e.sample_device(kind, dc.data_ptr(), dn.data_ptr(), batch, steps, mode, 0, do.data_ptr())
+        ts = []
+        for _ in range(iters):
+            e.sample_device(kind, dc.data_ptr(), dn.data_ptr(), batch, steps, mode, 0, do.data_ptr())
+            ts.append(e.last_device_ms)
+        ms = float(np.median(ts))
+        wbytes, nfe_flops = unet_bytes_and_flops(spec)
+        nfe = steps * per_step
+        gbs = wbytes * nfe / (ms * 1e-3) / 1e9
+        tflops = nfe_flops * batch * nfe / (ms * 1e-3) / 1e12
+        rows.append({"config": label, "device_p50_ms": round(ms, 3), "nfe": nfe,
+                     "actions_per_sec": round(batch * spec.horizon / (ms * 1e-3), 1),
+                     "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "tflops": round(tflops, 2),
+                     "fp32_mfma_frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "finite": bool(torch.isfinite(do).all().item())})
+        print(f"[bench] {label}: {ms:.3f} ms  ({gbs:.0f} GB/s weights, {tflops:.1f} TFLOP/s)",
+              file=sys.stderr, flush=True)
+    for e in engines.values():
+        e.close()
+    return rows
+
+
 def percentile(xs, q):
     import numpy as np
 
@@ -208,6 +263,7 @@ def main():
     ap.add_argument("--large-steps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the bimanual and flow configs")
     ap.add_argument("--roofline-iters", type=int, default=200,
                     help="rounds over the dominant convolution's layers")
     ap.add_argument("--roofline-only", action="store_true",
@@ -365,6 +421,8 @@ def main():
         "conv_breakdown_b1": [{k: v for k, v in r.items() if k != "indices"} for r in breakdown],
         "finite": bool(np.all(np.isfinite(action))),
     }
+    if not args.no_extra:
+        result["other_configs"] = extra_configs()
     if not args.no_cpu:
         cb = cpu_baseline(path, spec, args.cpu_budget)
         result["cpu_baseline"] = {

@@ -154,7 +154,10 @@ class Engine:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may already be unloaded
+            pass
 
     def __enter__(self):
         return self
