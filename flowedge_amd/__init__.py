@@ -33,7 +33,11 @@ EXPORTS = [
     "fe_engine_diffusion_denoise_batch", "fe_engine_sample_device", "fe_engine_prepare",
     "fe_engine_max_batch", "fe_engine_device_bytes", "fe_device_alloc_count",
     "fe_engine_last_device_ms", "fe_engine_conv_count", "fe_engine_conv_info",
-    "fe_engine_time_convs",
+    "fe_engine_time_convs", "fe_engine_flow_begin", "fe_engine_make_condition_metadata",
+    "fe_engine_flow_begin_request", "fe_engine_cancel_before", "fe_engine_flow_advance",
+    "fe_engine_flow_action_metadata", "fe_engine_diffusion_begin",
+    "fe_engine_diffusion_begin_generation", "fe_engine_diffusion_advance",
+    "fe_weights_model_digest",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -57,6 +61,24 @@ class ModelMetadata(ctypes.Structure):
                 ("d_state", ctypes.c_uint64), ("d_conv", ctypes.c_uint64),
                 ("action_dim", ctypes.c_uint64), ("condition_dim", ctypes.c_uint64),
                 ("decode_snapshot_bytes", ctypes.c_uint64)]
+
+
+class ConditionMetadata(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("protocol_version", ctypes.c_uint32),
+                ("solver", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("model_digest", ctypes.c_uint8 * 16), ("timestamp_ns", ctypes.c_uint64),
+                ("deadline_ns", ctypes.c_uint64), ("generation", ctypes.c_uint64),
+                ("condition_dim", ctypes.c_uint64), ("action_dim", ctypes.c_uint64),
+                ("solver_steps", ctypes.c_uint64), ("remaining_nfe", ctypes.c_uint64)]
+
+
+class ActionMetadata(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("protocol_version", ctypes.c_uint32),
+                ("solver", ctypes.c_uint32), ("status", ctypes.c_uint32),
+                ("model_digest", ctypes.c_uint8 * 16), ("timestamp_ns", ctypes.c_uint64),
+                ("deadline_ns", ctypes.c_uint64), ("generation", ctypes.c_uint64),
+                ("condition_dim", ctypes.c_uint64), ("action_dim", ctypes.c_uint64),
+                ("remaining_nfe", ctypes.c_uint64)]
 
 
 def lib():
@@ -110,12 +132,40 @@ def lib():
                                       ctypes.POINTER(u64)]
     L.fe_engine_time_convs.argtypes = [vp, ctypes.POINTER(sz), sz, sz, sz,
                                        ctypes.POINTER(ctypes.c_float)]
+    L.fe_engine_flow_begin.argtypes = [vp, _f32p, _f32p, sz, cint]
+    L.fe_engine_make_condition_metadata.argtypes = [vp, u64, u64, u64, sz, cint,
+                                                    ctypes.POINTER(ConditionMetadata)]
+    L.fe_engine_flow_begin_request.argtypes = [vp, _f32p, _f32p,
+                                               ctypes.POINTER(ConditionMetadata)]
+    L.fe_engine_cancel_before.restype = None
+    L.fe_engine_cancel_before.argtypes = [vp, u64]
+    L.fe_engine_flow_advance.argtypes = [vp, sz, _f32p, ctypes.POINTER(sz)]
+    L.fe_engine_flow_action_metadata.argtypes = [vp, ctypes.POINTER(ActionMetadata)]
+    L.fe_engine_diffusion_begin.argtypes = [vp, _f32p, _f32p, sz, cint, u64]
+    L.fe_engine_diffusion_begin_generation.argtypes = [vp, _f32p, _f32p, sz, cint, u64, u64]
+    L.fe_engine_diffusion_advance.argtypes = [vp, sz, _f32p, ctypes.POINTER(sz)]
+    L.fe_weights_model_digest.argtypes = [vp, ctypes.POINTER(ctypes.c_uint8 * 16)]
     _lib = L
     return L
 
 
 def last_error() -> str:
     return lib().fe_engine_last_error().decode()
+
+
+def weights_digest(path: str) -> str:
+    """Model digest (hex) of a checkpoint, computed on the host without a GPU."""
+    L = lib()
+    w = L.fe_weights_load(path.encode())
+    if not w:
+        raise RuntimeError(last_error())
+    try:
+        d = (ctypes.c_uint8 * 16)()
+        if L.fe_weights_model_digest(w, ctypes.byref(d)) != 0:
+            raise RuntimeError(last_error())
+        return _digest_hex(d)
+    finally:
+        L.fe_weights_free(w)
 
 
 def device_alloc_count() -> int:
@@ -131,6 +181,10 @@ def _arr(a, shape=None) -> np.ndarray:
 
 def _p(a: np.ndarray):
     return a.ctypes.data_as(_f32p)
+
+
+def _digest_hex(d) -> str:
+    return bytes(d).hex()
 
 
 class Engine:
@@ -196,8 +250,11 @@ class Engine:
         mm = ModelMetadata()
         if lib().fe_engine_model_metadata(self._h, ctypes.byref(mm)) != 0:
             raise RuntimeError(last_error())
-        return {"architecture": mm.architecture, "precision": mm.precision,
-                "action_dim": mm.action_dim, "condition_dim": mm.condition_dim}
+        return {"protocol_version": mm.protocol_version, "architecture": mm.architecture,
+                "precision": mm.precision, "model_digest": _digest_hex(mm.model_digest),
+                "d_model": mm.d_model, "n_layers": mm.n_layers, "action_dim": mm.action_dim,
+                "action_horizon": self.action_horizon, "condition_dim": mm.condition_dim,
+                "decode_snapshot_bytes": mm.decode_snapshot_bytes}
 
     @property
     def max_batch(self) -> int:
@@ -253,6 +310,73 @@ class Engine:
             raise RuntimeError("method must be 'euler', 'heun' or 'rk4'")
         self._check(lib().fe_engine_sample_condition(self._h, _p(c), _p(n), steps,
                                                      SOLVERS[method], _p(output)))
+
+    # ---- resumable solves (flowedge_ext.cc:564-623, 848-856) ----
+    def _output(self, output) -> None:
+        if not (isinstance(output, np.ndarray) and output.dtype == np.float32 and
+                output.flags["C_CONTIGUOUS"] and output.size == self._values()):
+            raise RuntimeError("output must be a contiguous float32 array of horizon*action_dim")
+
+    def flow_begin(self, condition, noise, steps: int = 10, method: str = "euler",
+                   generation: int | None = None, timestamp_ns: int = 0,
+                   deadline_ns: int = 0) -> None:
+        """Begin a resumable flow solve; with `generation`, a cancellable versioned request."""
+        c = _arr(condition, (self.condition_dim,))
+        n = _arr(noise, (self._values(),))
+        if method not in SOLVERS:
+            raise RuntimeError("method must be one of: euler, heun, rk4")
+        L = lib()
+        if generation is None:
+            self._check(L.fe_engine_flow_begin(self._h, _p(c), _p(n), steps, SOLVERS[method]))
+            return
+        md = ConditionMetadata()
+        self._check(L.fe_engine_make_condition_metadata(self._h, timestamp_ns, deadline_ns,
+                                                        generation, steps, SOLVERS[method],
+                                                        ctypes.byref(md)))
+        self._check(L.fe_engine_flow_begin_request(self._h, _p(c), _p(n), ctypes.byref(md)))
+
+    def flow_advance(self, output, step_budget: int = 1) -> int:
+        """Run at most `step_budget` solver steps into `output`; returns the steps remaining."""
+        self._output(output)
+        rem = ctypes.c_size_t()
+        self._check(lib().fe_engine_flow_advance(self._h, step_budget, _p(output),
+                                                 ctypes.byref(rem)))
+        return int(rem.value)
+
+    def cancel_before(self, generation: int) -> None:
+        lib().fe_engine_cancel_before(self._h, generation)
+
+    @property
+    def flow_metadata(self) -> dict:
+        md = ActionMetadata()
+        self._check(lib().fe_engine_flow_action_metadata(self._h, ctypes.byref(md)))
+        return {"protocol_version": md.protocol_version, "solver": md.solver,
+                "status": md.status, "model_digest": _digest_hex(md.model_digest),
+                "timestamp_ns": md.timestamp_ns, "deadline_ns": md.deadline_ns,
+                "generation": md.generation, "condition_dim": md.condition_dim,
+                "action_dim": md.action_dim, "remaining_nfe": md.remaining_nfe}
+
+    def diffusion_begin(self, condition, noise, steps: int = 10, scheduler: str = "ddim",
+                        seed: int = 0, generation: int | None = None) -> None:
+        """Begin a resumable DDIM/DDPM solve (extension); cancellable with `generation`."""
+        c = _arr(condition, (self.condition_dim,))
+        n = _arr(noise, (self._values(),))
+        if scheduler not in SCHEDULERS:
+            raise RuntimeError("scheduler must be 'ddim' or 'ddpm'")
+        L = lib()
+        if generation is None:
+            self._check(L.fe_engine_diffusion_begin(self._h, _p(c), _p(n), steps,
+                                                    SCHEDULERS[scheduler], seed))
+        else:
+            self._check(L.fe_engine_diffusion_begin_generation(
+                self._h, _p(c), _p(n), steps, SCHEDULERS[scheduler], seed, generation))
+
+    def diffusion_advance(self, output, step_budget: int = 1) -> int:
+        self._output(output)
+        rem = ctypes.c_size_t()
+        self._check(lib().fe_engine_diffusion_advance(self._h, step_budget, _p(output),
+                                                      ctypes.byref(rem)))
+        return int(rem.value)
 
     # ---- batched extensions ----
     def sample_diffusion_batch(self, condition, noise, steps: int = 10, scheduler: str = "ddim",

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <cmath>
 #include <cstdint>
@@ -258,6 +259,28 @@ struct FeEngine {
 
   std::list<GraphEntry> graphs;  // most recently used first
 
+  // Model identity (engine_runtime.cc:159-161).
+  std::array<std::uint8_t, 16> digest{};
+  std::uint32_t precision = 0;
+
+  // The one resumable solve of this engine (engine.h:321-366; engine_runtime.cc:494-561).
+  // `graphs[0]` starts the solve from the input buffers, `graphs[1 + i]` runs step i and writes
+  // the current action; they are kept while later solves have the same kind, step count and mode.
+  // Any other sampling or denoising call reuses the state buffers and ends the solve.
+  struct Solve {
+    bool active = false, cancelled = false, tracking = false;
+    int kind = 0, mode = 0;
+    std::size_t steps = 0, next = 0;
+    std::uint64_t timestamp_ns = 0, deadline_ns = 0, generation = 0;
+    int g_kind = -1, g_mode = -1;
+    std::size_t g_steps = 0;
+    std::vector<hipGraphExec_t> graphs;
+    std::size_t remaining() const { return steps - next; }
+  } solve;
+  // Highest generation announced by fe_engine_cancel_before or a tracked begin; the only state
+  // another thread may touch while a solve advances.
+  std::atomic<std::uint64_t> latest_generation{0};
+
   // Diagnostics: every fused convolution of one U-Net evaluation, recorded from an eager run.
   struct ConvRecord {
     std::string name;
@@ -280,6 +303,8 @@ struct FeEngine {
   ~FeEngine() {
     for (auto& g : graphs)
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    for (hipGraphExec_t g : solve.graphs)
+      if (g) (void)hipGraphExecDestroy(g);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -288,9 +313,17 @@ struct FeEngine {
   }
 };
 
+// ABI layouts fixed by protocol/contracts.h:139-142.
+static_assert(sizeof(fe_model_digest) == 16);
+static_assert(sizeof(fe_model_metadata) == 96);
+static_assert(sizeof(fe_condition_metadata) == 88);
+static_assert(sizeof(fe_action_metadata) == 80);
+
 namespace {
 
 constexpr std::size_t kGraphCache = 32;
+
+void end_solve(FeEngine* e);
 
 // Sizing and validation of the weights; fills the slots and offsets.
 struct Builder {
@@ -966,70 +999,95 @@ hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int
   return enqueue_film_cond(e, batch);
 }
 
-// Whole DDIM/DDPM sampling call (diffusion.cc:916-1035) for `batch` samples.
-hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int scheduler,
-                             const float* alphas) {
+// DDIM/DDPM sampling (diffusion.cc:916-1035) for `batch` samples, in three parts so that a
+// resumable solve can replay them separately: the start (noise into the state, FiLM condition
+// part), step i, and the readout of the current action (unnormalised state).
+hipError_t enqueue_diffusion_start(FeEngine& e, int batch) {
+  using namespace fe::hip;
+  const Config& c = e.cfg;
+  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
+                      static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
+  return enqueue_film_cond(e, batch);
+}
+
+hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int scheduler,
+                                  const float* alphas, std::size_t i) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   const std::size_t ratio = c.train_timesteps / steps;
-  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
-                      static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
-  FE_TRY(enqueue_film_cond(e, batch));
-  std::uint64_t noisy_steps = 0;
-  for (std::size_t i = 0; i < steps; ++i) {
-    const std::size_t t = (steps - 1 - i) * ratio;
-    const std::ptrdiff_t prev = static_cast<std::ptrdiff_t>(t) - static_cast<std::ptrdiff_t>(ratio);
-    const float at = alphas[t];
-    const float ap = prev >= 0 ? alphas[prev] : 1.0f;
-    const float bt = 1.0f - at;
-    UpdateOp u{};
-    u.x = e.ptr(e.x_state);
-    u.xin = e.ptr(e.x_in);
-    u.sqrt_at = std::sqrt(at);
-    u.sqrt_bt = std::sqrt(bt);
-    u.clip = c.clip ? 1 : 0;
-    u.clip_range = c.clip_range;
-    if (scheduler == FE_DIFFUSION_DDIM) {
-      u.kind = kUpdateDDIM;
-      u.sqrt_ap = std::sqrt(ap);
-      u.sqrt_1map = std::sqrt(1.0f - ap);
-    } else {
-      // diffusion.cc:1006-1023.
-      const float ca = at / ap, cb = 1.0f - ca;
-      u.kind = kUpdateDDPM;
-      u.coef_x0 = std::sqrt(ap) * cb / std::max(bt, 1e-20f);
-      u.coef_x = std::sqrt(ca) * (1.0f - ap) / std::max(bt, 1e-20f);
-      const float var = ((1.0f - ap) / std::max(bt, 1e-20f)) * cb;
-      u.sigma = std::sqrt(std::max(var, 1e-20f));
-      u.seed = e.ptr<std::uint64_t>(e.seed_dev);
-      u.add_noise = prev >= 0 ? 1 : 0;
-      u.noise_offset = noisy_steps * e.values;
-      if (prev >= 0) ++noisy_steps;
-    }
-    const float* row = e.ptr(e.ddim_table) + t * e.film_total;
-    FE_TRY(enqueue_unet(e, batch, row, u));
+  const std::size_t t = (steps - 1 - i) * ratio;
+  const std::ptrdiff_t prev = static_cast<std::ptrdiff_t>(t) - static_cast<std::ptrdiff_t>(ratio);
+  const float at = alphas[t];
+  const float ap = prev >= 0 ? alphas[prev] : 1.0f;
+  const float bt = 1.0f - at;
+  UpdateOp u{};
+  u.x = e.ptr(e.x_state);
+  u.xin = e.ptr(e.x_in);
+  u.sqrt_at = std::sqrt(at);
+  u.sqrt_bt = std::sqrt(bt);
+  u.clip = c.clip ? 1 : 0;
+  u.clip_range = c.clip_range;
+  if (scheduler == FE_DIFFUSION_DDIM) {
+    u.kind = kUpdateDDIM;
+    u.sqrt_ap = std::sqrt(ap);
+    u.sqrt_1map = std::sqrt(1.0f - ap);
+  } else {
+    // diffusion.cc:1006-1023.  Only the last step (t < ratio) draws no noise, so step i starts at
+    // Gaussian draw i * H * A of the sample's stream.
+    const float ca = at / ap, cb = 1.0f - ca;
+    u.kind = kUpdateDDPM;
+    u.coef_x0 = std::sqrt(ap) * cb / std::max(bt, 1e-20f);
+    u.coef_x = std::sqrt(ca) * (1.0f - ap) / std::max(bt, 1e-20f);
+    const float var = ((1.0f - ap) / std::max(bt, 1e-20f)) * cb;
+    u.sigma = std::sqrt(std::max(var, 1e-20f));
+    u.seed = e.ptr<std::uint64_t>(e.seed_dev);
+    u.add_noise = prev >= 0 ? 1 : 0;
+    u.noise_offset = static_cast<std::uint64_t>(i) * e.values;
   }
-  return finish_sample(e.ptr(e.x_state), e.ptr(e.amin), e.ptr(e.amax), e.ptr(e.out_action), batch,
-                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream);
+  const float* row = e.ptr(e.ddim_table) + t * e.film_total;
+  return enqueue_unet(e, batch, row, u);
 }
 
-// Flow-ODE sampling (flow.cc:291-318) with the U-Net as velocity field.
-hipError_t enqueue_flow(FeEngine& e, int batch, std::size_t steps, int method) {
+hipError_t enqueue_diffusion_readout(FeEngine& e, int batch) {
+  const Config& c = e.cfg;
+  return fe::hip::finish_sample(e.ptr(e.x_state), e.ptr(e.amin), e.ptr(e.amax),
+                                e.ptr(e.out_action), batch, static_cast<int>(c.horizon),
+                                static_cast<int>(c.action_dim), e.stream);
+}
+
+hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int scheduler,
+                             const float* alphas) {
+  FE_TRY(enqueue_diffusion_start(e, batch));
+  for (std::size_t i = 0; i < steps; ++i)
+    FE_TRY(enqueue_diffusion_step(e, batch, steps, scheduler, alphas, i));
+  return enqueue_diffusion_readout(e, batch);
+}
+
+// Flow-ODE sampling (flow.cc:291-318) with the U-Net as velocity field, in the same three parts:
+// the start also computes the FiLM time rows of every evaluation of the solve.
+std::size_t flow_stages(int method) {
+  return method == FE_SOLVER_RK4 ? 4 : (method == FE_SOLVER_HEUN ? 2 : 1);
+}
+
+hipError_t enqueue_flow_start(FeEngine& e, int batch, std::size_t steps, int method) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
-  const int stages = method == FE_SOLVER_RK4 ? 4 : (method == FE_SOLVER_HEUN ? 2 : 1);
   TimeSpec ts;
   ts.mode = kTimesFlow;
   ts.steps = static_cast<int>(steps);
   ts.method = method;
-  const int nfe = static_cast<int>(steps) * stages;
-  FE_TRY(enqueue_film(e, ts, nfe, batch));
+  return enqueue_film(e, ts, static_cast<int>(steps * flow_stages(method)), batch);
+}
+
+hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int method,
+                             std::size_t step) {
+  using namespace fe::hip;
+  const int stages = static_cast<int>(flow_stages(method));
   const float dt = 1.0f / static_cast<float>(steps);
   const float half_dt = 0.5f * dt;
-  for (int n = 0; n < nfe; ++n) {
-    const int j = n % stages;
+  for (int j = 0; j < stages; ++j) {
     UpdateOp u{};
     u.x = e.ptr(e.x_state);
     u.xin = e.ptr(e.x_in);
@@ -1054,11 +1112,24 @@ hipError_t enqueue_flow(FeEngine& e, int batch, std::size_t steps, int method) {
         u.kind = kUpdateRK4;
       }
     }
-    FE_TRY(enqueue_unet(e, batch, e.ptr(e.film_table) + static_cast<std::size_t>(n) * e.film_total,
-                        u));
+    const std::size_t n = step * static_cast<std::size_t>(stages) + static_cast<std::size_t>(j);
+    FE_TRY(enqueue_unet(e, batch, e.ptr(e.film_table) + n * e.film_total, u));
   }
-  return finish_sample(e.ptr(e.x_state), nullptr, nullptr, e.ptr(e.out_action), batch,
-                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream);
+  return hipSuccess;
+}
+
+hipError_t enqueue_flow_readout(FeEngine& e, int batch) {
+  // flow.cc:321: the flow head returns x(1) as is (no unnormalisation).
+  const Config& c = e.cfg;
+  return fe::hip::finish_sample(e.ptr(e.x_state), nullptr, nullptr, e.ptr(e.out_action), batch,
+                                static_cast<int>(c.horizon), static_cast<int>(c.action_dim),
+                                e.stream);
+}
+
+hipError_t enqueue_flow(FeEngine& e, int batch, std::size_t steps, int method) {
+  FE_TRY(enqueue_flow_start(e, batch, steps, method));
+  for (std::size_t s = 0; s < steps; ++s) FE_TRY(enqueue_flow_step(e, batch, steps, method, s));
+  return enqueue_flow_readout(e, batch);
 }
 
 std::vector<float> alphas_cumprod(std::size_t T) {
@@ -1079,6 +1150,24 @@ std::vector<float> alphas_cumprod(std::size_t T) {
   return a;
 }
 
+// Captures what `body` enqueues on the engine stream into an instantiated graph.
+template <typename Body>
+hipError_t capture_graph(FeEngine& e, Body&& body, hipGraphExec_t& exec) {
+  exec = nullptr;
+  FE_TRY(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal));
+  hipError_t st = body();
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(e.stream, &graph);
+  if (st != hipSuccess || end != hipSuccess) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return st != hipSuccess ? st : end;
+  }
+  st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (st != hipSuccess) exec = nullptr;
+  return st;
+}
+
 // Returns the cached graph for this shape, capturing it on first use.
 hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps, int mode,
                      hipGraphExec_t& exec) {
@@ -1088,24 +1177,17 @@ hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps
       exec = it->exec;
       return hipSuccess;
     }
-  FE_TRY(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal));
-  hipError_t st;
-  if (kind == 0) {
-    const std::vector<float> alphas = alphas_cumprod(e.cfg.train_timesteps);
-    st = enqueue_diffusion(e, static_cast<int>(batch), steps, mode, alphas.data());
-  } else {
-    st = enqueue_flow(e, static_cast<int>(batch), steps, mode);
-  }
-  hipGraph_t graph = nullptr;
-  const hipError_t end = hipStreamEndCapture(e.stream, &graph);
-  if (st != hipSuccess || end != hipSuccess) {
-    if (graph) (void)hipGraphDestroy(graph);
-    return st != hipSuccess ? st : end;
-  }
   hipGraphExec_t inst = nullptr;
-  st = hipGraphInstantiate(&inst, graph, nullptr, nullptr, 0);
-  (void)hipGraphDestroy(graph);
-  if (st != hipSuccess) return st;
+  FE_TRY(capture_graph(
+      e,
+      [&]() {
+        if (kind == 0) {
+          const std::vector<float> alphas = alphas_cumprod(e.cfg.train_timesteps);
+          return enqueue_diffusion(e, static_cast<int>(batch), steps, mode, alphas.data());
+        }
+        return enqueue_flow(e, static_cast<int>(batch), steps, mode);
+      },
+      inst));
   if (e.graphs.size() >= kGraphCache) {
     (void)hipGraphExecDestroy(e.graphs.back().exec);
     e.graphs.pop_back();
@@ -1134,6 +1216,7 @@ int ensure_conv_records(FeEngine* e) {
   UpdateOp u{};
   u.kind = kUpdateDenoise;
   u.out = e->ptr(e->out_action);
+  end_solve(e);
   e->recording = true;
   st = enqueue_film(*e, ts, 1, 1);
   if (st == hipSuccess) st = enqueue_unet(*e, 1, e->ptr(e->film_table), u);
@@ -1199,6 +1282,7 @@ int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, st
                 std::size_t steps, int mode, std::uint64_t seed, float* action) {
   const int rc = check_sample(e, kind, batch, steps, mode);
   if (rc != FE_STATUS_OK) return rc;
+  end_solve(e);
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) return hip_fail("hipSetDevice", st);
   const Config& c = e->cfg;
@@ -1221,6 +1305,168 @@ int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, st
     return hip_fail("Sampling failed", st);
   std::memcpy(action, e->pin_action, nv * 4);
   return FE_STATUS_OK;
+}
+
+// ---- Resumable solves (engine.h:321-366, engine_runtime.cc:494-561, flow.cc:210-318) ----
+
+void drop_solve_graphs(FeEngine::Solve& v) {
+  for (hipGraphExec_t g : v.graphs)
+    if (g) (void)hipGraphExecDestroy(g);
+  v.graphs.clear();
+  v.g_kind = v.g_mode = -1;
+  v.g_steps = 0;
+}
+
+// Ends the resumable solve because another call is about to reuse its state buffers.
+void end_solve(FeEngine* e) {
+  FeEngine::Solve& v = e->solve;
+  v.active = v.cancelled = v.tracking = false;
+  v.steps = v.next = 0;
+}
+
+// Raises the engine's latest generation to `generation` (engine_runtime.cc:512-519, 554-561).
+void raise_generation(FeEngine* e, std::uint64_t generation) {
+  std::uint64_t seen = e->latest_generation.load(std::memory_order_relaxed);
+  while (seen < generation &&
+         !e->latest_generation.compare_exchange_weak(seen, generation, std::memory_order_release,
+                                                     std::memory_order_relaxed)) {
+  }
+}
+
+// Step graphs of one batch-1 solve shape: [0] = start + readout, [1 + i] = step i + readout.
+hipError_t build_solve_graphs(FeEngine& e, int kind, std::size_t steps, int mode) {
+  FeEngine::Solve& v = e.solve;
+  if (v.g_kind == kind && v.g_steps == steps && v.g_mode == mode) return hipSuccess;
+  drop_solve_graphs(v);
+  const std::vector<float> alphas =
+      kind == 0 ? alphas_cumprod(e.cfg.train_timesteps) : std::vector<float>();
+  v.graphs.reserve(steps + 1);
+  for (std::size_t g = 0; g <= steps; ++g) {
+    hipGraphExec_t exec = nullptr;
+    const hipError_t st = capture_graph(
+        e,
+        [&]() -> hipError_t {
+          if (kind == 0) {
+            FE_TRY(g == 0 ? enqueue_diffusion_start(e, 1)
+                          : enqueue_diffusion_step(e, 1, steps, mode, alphas.data(), g - 1));
+            return enqueue_diffusion_readout(e, 1);
+          }
+          FE_TRY(g == 0 ? enqueue_flow_start(e, 1, steps, mode)
+                        : enqueue_flow_step(e, 1, steps, mode, g - 1));
+          return enqueue_flow_readout(e, 1);
+        },
+        exec);
+    if (st != hipSuccess) {
+      drop_solve_graphs(v);
+      return st;
+    }
+    v.graphs.push_back(exec);
+  }
+  v.g_kind = kind;
+  v.g_steps = steps;
+  v.g_mode = mode;
+  return hipSuccess;
+}
+
+struct SolveRequest {
+  int kind = 0, mode = 0;
+  std::size_t steps = 0;
+  std::uint64_t seed = 0;
+  bool tracking = false;
+  std::uint64_t generation = 0, timestamp_ns = 0, deadline_ns = 0;
+};
+
+int solve_begin(FeEngine* e, const float* cond, const float* noise, const SolveRequest& r) {
+  const int rc = check_sample(e, r.kind, 1, r.steps, r.mode);
+  if (rc != FE_STATUS_OK) return rc;
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  end_solve(e);
+  FeEngine::Solve& v = e->solve;
+  v.kind = r.kind;
+  v.mode = r.mode;
+  v.tracking = r.tracking;
+  v.generation = r.generation;
+  v.timestamp_ns = r.timestamp_ns;
+  v.deadline_ns = r.deadline_ns;
+  if (r.tracking) raise_generation(e, r.generation);
+  const char* const failed = r.kind == 1 ? "Failed to initialize resumable flow sampler"
+                                         : "Failed to initialize resumable diffusion sampler";
+  if ((st = build_solve_graphs(*e, r.kind, r.steps, r.mode)) != hipSuccess)
+    return hip_fail(failed, st);
+  std::memcpy(e->pin_cond, cond, e->cfg.cond_dim * 4);
+  std::memcpy(e->pin_noise, noise, e->values * 4);
+  *e->pin_seed = r.seed;
+  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), e->pin_cond, e->cfg.cond_dim * 4,
+                           hipMemcpyHostToDevice, e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->in_noise), e->pin_noise, e->values * 4,
+                           hipMemcpyHostToDevice, e->stream)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->ptr(e->seed_dev), e->pin_seed, 8, hipMemcpyHostToDevice,
+                           e->stream)) != hipSuccess ||
+      (st = hipGraphLaunch(v.graphs[0], e->stream)) != hipSuccess ||
+      (st = hipStreamSynchronize(e->stream)) != hipSuccess)
+    return hip_fail(failed, st);
+  v.steps = r.steps;
+  v.next = 0;
+  v.active = true;
+  return FE_STATUS_OK;
+}
+
+// Runs at most `budget` steps and copies the current action out (flow.cc:260-318).  A tracked
+// solve checks for cancellation before every step and waits for each step, so that a
+// cancellation from another thread stops it at the next step boundary.
+int solve_advance(FeEngine* e, int kind, std::size_t budget, float* action,
+                  std::size_t& remaining) {
+  FeEngine::Solve& v = e->solve;
+  // Messages as engine_runtime.cc:535-550 for flow solves.
+  const char* const cancelled = kind == 1 ? "Flow solve was cancelled by a newer generation"
+                                          : "Diffusion solve was cancelled by a newer generation";
+  if (v.cancelled) {
+    set_error(cancelled);
+    remaining = v.remaining();
+    return FE_STATUS_CANCELLED;
+  }
+  if (!v.active || v.kind != kind) {
+    set_error(kind == 1 ? "No resumable flow sample is active"
+                        : "No resumable diffusion sample is active");
+    return FE_STATUS_NO_ACTIVE_OPERATION;
+  }
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  const std::size_t todo = std::min(budget, v.remaining());
+  for (std::size_t k = 0; k < todo; ++k) {
+    if (v.tracking && e->latest_generation.load(std::memory_order_acquire) > v.generation) {
+      v.cancelled = true;
+      v.active = false;
+      break;
+    }
+    if ((st = hipGraphLaunch(v.graphs[1 + v.next], e->stream)) != hipSuccess ||
+        (v.tracking && (st = hipStreamSynchronize(e->stream)) != hipSuccess)) {
+      v.active = false;
+      return hip_fail("Resumable sampler step failed", st);
+    }
+    ++v.next;
+  }
+  const std::size_t nv = e->values;
+  if ((st = hipMemcpyAsync(e->pin_action, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToHost,
+                           e->stream)) != hipSuccess ||
+      (st = hipStreamSynchronize(e->stream)) != hipSuccess) {
+    v.active = false;
+    return hip_fail("Resumable sampler step failed", st);
+  }
+  std::memcpy(action, e->pin_action, nv * 4);
+  remaining = v.remaining();
+  if (v.cancelled) {
+    set_error(cancelled);
+    return FE_STATUS_CANCELLED;
+  }
+  return FE_STATUS_OK;
+}
+
+// Evaluations per solver step (engine.cc:51-59); a DDIM/DDPM step is one evaluation.
+std::uint64_t nfe_for(std::size_t steps, int kind, int mode) {
+  const std::uint64_t per = kind == 1 ? flow_stages(mode) : 1;
+  return steps > UINT64_MAX / per ? UINT64_MAX : static_cast<std::uint64_t>(steps) * per;
 }
 
 // Smallest batch that runs the convolutions on the matrix cores (FLOWEDGE_MFMA_BATCH; 0 = by
@@ -1277,6 +1523,8 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     return nullptr;
   }
   e->values = e->cfg.horizon * e->cfg.action_dim;
+  e->digest = ck->digest();
+  e->precision = ck->precision();
   Builder builder{*e, *ck, Plan{}, {}};
   if (!builder.build()) {
     set_error(builder.err);
@@ -1372,6 +1620,16 @@ size_t fe_weights_size_bytes(const fe_weights* weights) {
 
 void fe_weights_free(fe_weights* weights) { delete weights; }
 
+int fe_weights_model_digest(const fe_weights* weights, fe_model_digest* digest) {
+  clear_error();
+  if (weights == nullptr || weights->ck == nullptr || digest == nullptr) {
+    set_error("Invalid arguments to fe_weights_model_digest");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  std::memcpy(digest->bytes, weights->ck->digest().data(), FE_MODEL_DIGEST_BYTES);
+  return FE_STATUS_OK;
+}
+
 static bool env_threads(unsigned& out) {
   const char* v = std::getenv("FLOWEDGE_THREADS");
   if (v == nullptr || *v == '\0') {
@@ -1460,7 +1718,8 @@ int fe_engine_model_metadata(const fe_engine* engine, fe_model_metadata* metadat
   m.struct_size = sizeof(m);
   m.protocol_version = FE_PROTOCOL_VERSION;
   m.architecture = FE_ARCH_DIFFUSION_HEAD;
-  m.precision = engine->any_bf16 ? FE_PRECISION_MIXED : FE_PRECISION_F32;
+  m.precision = engine->precision;
+  std::memcpy(m.model_digest.bytes, engine->digest.data(), FE_MODEL_DIGEST_BYTES);
   m.action_dim = engine->cfg.action_dim;
   m.condition_dim = engine->cfg.cond_dim;
   *metadata = m;
@@ -1559,6 +1818,7 @@ int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
   FeEngine* e = engine;
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  end_solve(e);
   const Config& c = e->cfg;
   const std::size_t nc = batch * c.cond_dim, nv = batch * e->values;
   std::memcpy(e->pin_cond, condition, nc * 4);
@@ -1610,6 +1870,7 @@ int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_
   if (rc != FE_STATUS_OK) return rc;
   hipError_t st = hipSetDevice(e->device);
   if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  end_solve(e);
   const std::size_t nc = batch * e->cfg.cond_dim, nv = batch * e->values;
   *e->pin_seed = seed;
   if ((st = hipMemcpyAsync(e->ptr(e->in_cond), condition_dev, nc * 4, hipMemcpyDeviceToDevice,
@@ -1641,6 +1902,190 @@ int fe_engine_prepare(fe_engine* engine, int kind, size_t batch, size_t steps, i
   hipGraphExec_t exec = nullptr;
   st = get_graph(*engine, kind, batch, steps, mode, exec);
   return st == hipSuccess ? FE_STATUS_OK : hip_fail("Failed to build sampling graph", st);
+}
+
+// ---- Resumable solves (engine.h:321-366) ----
+
+int fe_engine_flow_begin(fe_engine* engine, const float* condition, const float* noise,
+                         size_t steps, int method) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || noise == nullptr || steps == 0) {
+    set_error("Invalid arguments to fe_engine_flow_begin");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (method < FE_SOLVER_EULER || method > FE_SOLVER_RK4) {
+    set_error("Invalid solver method");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  SolveRequest r;
+  r.kind = 1;
+  r.mode = method;
+  r.steps = steps;
+  return solve_begin(engine, condition, noise, r);
+}
+
+int fe_engine_make_condition_metadata(const fe_engine* engine, uint64_t timestamp_ns,
+                                      uint64_t deadline_ns, uint64_t generation, size_t steps,
+                                      int method, fe_condition_metadata* metadata) {
+  clear_error();
+  if (engine == nullptr || metadata == nullptr || steps == 0 ||
+      (deadline_ns != 0 && deadline_ns < timestamp_ns)) {
+    set_error("Invalid arguments to fe_engine_make_condition_metadata");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (method < FE_SOLVER_EULER || method > FE_SOLVER_RK4) {
+    set_error("Invalid solver method");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  fe_condition_metadata m{};
+  m.struct_size = sizeof(m);
+  m.protocol_version = FE_PROTOCOL_VERSION;
+  m.solver = static_cast<uint32_t>(method);
+  std::memcpy(m.model_digest.bytes, engine->digest.data(), FE_MODEL_DIGEST_BYTES);
+  m.timestamp_ns = timestamp_ns;
+  m.deadline_ns = deadline_ns;
+  m.generation = generation;
+  m.condition_dim = engine->cfg.cond_dim;
+  m.action_dim = engine->cfg.action_dim;
+  m.solver_steps = steps;
+  m.remaining_nfe = nfe_for(steps, 1, method);
+  *metadata = m;
+  return FE_STATUS_OK;
+}
+
+int fe_engine_flow_begin_request(fe_engine* engine, const float* condition, const float* noise,
+                                 const fe_condition_metadata* metadata) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || noise == nullptr || metadata == nullptr ||
+      metadata->struct_size < sizeof(*metadata) ||
+      metadata->protocol_version != FE_PROTOCOL_VERSION || metadata->reserved != 0 ||
+      metadata->solver_steps == 0 || metadata->solver_steps > SIZE_MAX) {
+    set_error("Invalid versioned flow request metadata");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const int method = static_cast<int>(metadata->solver);
+  if (metadata->solver > static_cast<uint32_t>(FE_SOLVER_RK4)) {
+    set_error("Invalid solver method in flow request metadata");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  if (std::memcmp(metadata->model_digest.bytes, engine->digest.data(), FE_MODEL_DIGEST_BYTES) !=
+          0 ||
+      metadata->condition_dim != engine->cfg.cond_dim ||
+      metadata->action_dim != engine->cfg.action_dim ||
+      metadata->remaining_nfe != nfe_for(static_cast<size_t>(metadata->solver_steps), 1, method) ||
+      (metadata->deadline_ns != 0 && metadata->deadline_ns < metadata->timestamp_ns)) {
+    set_error("Flow request metadata is incompatible with this model");
+    return FE_STATUS_INCOMPATIBLE_STATE;
+  }
+  SolveRequest r;
+  r.kind = 1;
+  r.mode = method;
+  r.steps = static_cast<size_t>(metadata->solver_steps);
+  r.tracking = true;
+  r.generation = metadata->generation;
+  r.timestamp_ns = metadata->timestamp_ns;
+  r.deadline_ns = metadata->deadline_ns;
+  return solve_begin(engine, condition, noise, r);
+}
+
+void fe_engine_cancel_before(fe_engine* engine, uint64_t generation) {
+  if (engine != nullptr) raise_generation(engine, generation);
+}
+
+int fe_engine_flow_advance(fe_engine* engine, size_t step_budget, float* action,
+                           size_t* steps_remaining) {
+  clear_error();
+  if (engine == nullptr || action == nullptr || step_budget == 0) {
+    set_error("Invalid arguments to fe_engine_flow_advance");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  size_t remaining = 0;
+  const int rc = solve_advance(engine, 1, step_budget, action, remaining);
+  if ((rc == FE_STATUS_OK || rc == FE_STATUS_CANCELLED) && steps_remaining != nullptr)
+    *steps_remaining = remaining;
+  return rc;
+}
+
+int fe_engine_flow_action_metadata(const fe_engine* engine, fe_action_metadata* metadata) {
+  clear_error();
+  if (engine == nullptr || metadata == nullptr) {
+    set_error("Invalid arguments to fe_engine_flow_action_metadata");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const FeEngine::Solve& v = engine->solve;
+  fe_action_metadata m{};
+  m.struct_size = sizeof(m);
+  m.protocol_version = FE_PROTOCOL_VERSION;
+  m.solver = static_cast<uint32_t>(v.mode);
+  // engine_runtime.cc:294-301.
+  m.status = v.cancelled ? FE_ACTION_CANCELLED
+             : !v.active ? FE_ACTION_FAILED
+             : v.remaining() == 0 ? FE_ACTION_COMPLETE
+                                  : FE_ACTION_RUNNING;
+  std::memcpy(m.model_digest.bytes, engine->digest.data(), FE_MODEL_DIGEST_BYTES);
+  m.timestamp_ns = v.timestamp_ns;
+  m.deadline_ns = v.deadline_ns;
+  m.generation = v.generation;
+  m.condition_dim = engine->cfg.cond_dim;
+  m.action_dim = engine->cfg.action_dim;
+  m.remaining_nfe = nfe_for(v.remaining(), v.kind, v.mode);
+  *metadata = m;
+  return FE_STATUS_OK;
+}
+
+int fe_engine_diffusion_begin(fe_engine* engine, const float* condition, const float* noise,
+                              size_t steps, int scheduler, uint64_t seed) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || noise == nullptr || steps == 0) {
+    set_error("Invalid arguments to fe_engine_diffusion_begin");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (scheduler != FE_DIFFUSION_DDIM && scheduler != FE_DIFFUSION_DDPM) {
+    set_error("Diffusion scheduler must be FE_DIFFUSION_DDIM or FE_DIFFUSION_DDPM");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  SolveRequest r;
+  r.kind = 0;
+  r.mode = scheduler;
+  r.steps = steps;
+  r.seed = seed;
+  return solve_begin(engine, condition, noise, r);
+}
+
+int fe_engine_diffusion_begin_generation(fe_engine* engine, const float* condition,
+                                         const float* noise, size_t steps, int scheduler,
+                                         uint64_t seed, uint64_t generation) {
+  clear_error();
+  if (engine == nullptr || condition == nullptr || noise == nullptr || steps == 0) {
+    set_error("Invalid arguments to fe_engine_diffusion_begin_generation");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  if (scheduler != FE_DIFFUSION_DDIM && scheduler != FE_DIFFUSION_DDPM) {
+    set_error("Diffusion scheduler must be FE_DIFFUSION_DDIM or FE_DIFFUSION_DDPM");
+    return FE_STATUS_INVALID_SOLVER;
+  }
+  SolveRequest r;
+  r.kind = 0;
+  r.mode = scheduler;
+  r.steps = steps;
+  r.seed = seed;
+  r.tracking = true;
+  r.generation = generation;
+  return solve_begin(engine, condition, noise, r);
+}
+
+int fe_engine_diffusion_advance(fe_engine* engine, size_t step_budget, float* action,
+                                size_t* steps_remaining) {
+  clear_error();
+  if (engine == nullptr || action == nullptr || step_budget == 0) {
+    set_error("Invalid arguments to fe_engine_diffusion_advance");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  size_t remaining = 0;
+  const int rc = solve_advance(engine, 0, step_budget, action, remaining);
+  if ((rc == FE_STATUS_OK || rc == FE_STATUS_CANCELLED) && steps_remaining != nullptr)
+    *steps_remaining = remaining;
+  return rc;
 }
 
 size_t fe_engine_max_batch(const fe_engine* engine) {

@@ -1,5 +1,7 @@
 #include "safetensors.h"
 
+#include "identity.h"
+
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -7,6 +9,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <thread>
 #include <utility>
 
 namespace fe {
@@ -153,6 +156,9 @@ std::shared_ptr<const Checkpoint> Checkpoint::open(const char* path, std::string
     error = "malformed safetensors header";
     return nullptr;
   }
+  const unsigned hw = std::thread::hardware_concurrency();
+  ck->digest_ = fingerprint_tensors(ck->tensors_, std::min(hw == 0 ? 1u : hw, 8u));
+  ck->precision_ = checkpoint_precision(ck->tensors_);
   return ck;
 }
 

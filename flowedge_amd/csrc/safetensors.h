@@ -6,6 +6,7 @@
 // prod(shape) * element size, spans must lie inside the data section and must not overlap.
 #pragma once
 
+#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <memory>
@@ -39,6 +40,9 @@ class Checkpoint {
   const TensorInfo* find(const std::string& name) const;
   const std::vector<TensorInfo>& tensors() const { return tensors_; }
   std::size_t weight_bytes() const { return weight_bytes_; }
+  // Model fingerprint and FE_PRECISION_* class, computed once at open.
+  const std::array<std::uint8_t, 16>& digest() const { return digest_; }
+  std::uint32_t precision() const { return precision_; }
 
  private:
   Checkpoint() = default;
@@ -46,6 +50,8 @@ class Checkpoint {
   std::size_t map_size_ = 0;
   std::vector<TensorInfo> tensors_;
   std::size_t weight_bytes_ = 0;
+  std::array<std::uint8_t, 16> digest_{};
+  std::uint32_t precision_ = 0;
 };
 
 }  // namespace fe

@@ -52,6 +52,14 @@ enum {
   FE_PRECISION_MIXED = 3,
 };
 
+/* protocol/contracts.h:36-42 — status of a resumable solve's current action. */
+enum {
+  FE_ACTION_RUNNING = 0,
+  FE_ACTION_COMPLETE = 1,
+  FE_ACTION_CANCELLED = 2,
+  FE_ACTION_FAILED = 3,
+};
+
 /* engine.h:29-43 */
 typedef struct fe_diffusion_metadata {
   uint32_t struct_size;
@@ -87,6 +95,35 @@ typedef struct fe_model_metadata {
   uint64_t condition_dim;
   uint64_t decode_snapshot_bytes;
 } fe_model_metadata;
+
+/* protocol/contracts.h:105-134 — versioned request and action metadata of resumable solves. */
+typedef struct fe_condition_metadata {
+  uint32_t struct_size;
+  uint32_t protocol_version;
+  uint32_t solver;
+  uint32_t reserved;
+  fe_model_digest model_digest;
+  uint64_t timestamp_ns;
+  uint64_t deadline_ns;
+  uint64_t generation;
+  uint64_t condition_dim;
+  uint64_t action_dim;
+  uint64_t solver_steps;
+  uint64_t remaining_nfe;
+} fe_condition_metadata;
+typedef struct fe_action_metadata {
+  uint32_t struct_size;
+  uint32_t protocol_version;
+  uint32_t solver;
+  uint32_t status;
+  fe_model_digest model_digest;
+  uint64_t timestamp_ns;
+  uint64_t deadline_ns;
+  uint64_t generation;
+  uint64_t condition_dim;
+  uint64_t action_dim;
+  uint64_t remaining_nfe;
+} fe_action_metadata;
 
 /* engine.h:46-59 */
 enum {
@@ -165,6 +202,36 @@ int fe_engine_diffusion_denoise(fe_engine* engine, const float* condition,
 int fe_engine_sample_condition(fe_engine* engine, const float* condition, const float* noise,
                                size_t steps, int method, float* action);
 
+/* engine.h:321-330 — begin a resumable flow solve (velocity checkpoints, as
+ * fe_engine_sample_condition).  One resumable solve per engine: a new begin replaces it, and any
+ * sampling or denoising call on the engine ends it (its buffers are reused).  Not cancellable. */
+int fe_engine_flow_begin(fe_engine* engine, const float* condition, const float* noise,
+                         size_t steps, int method);
+
+/* engine.h:332-338 — request metadata for this model: digest, dimensions (action_dim per horizon
+ * step), steps and remaining_nfe = steps x evaluations per step. */
+int fe_engine_make_condition_metadata(const fe_engine* engine, uint64_t timestamp_ns,
+                                      uint64_t deadline_ns, uint64_t generation, size_t steps,
+                                      int method, fe_condition_metadata* metadata);
+
+/* engine.h:340-342 — begin a cancellable flow solve after validating the metadata
+ * (status 9 if it does not match this model). */
+int fe_engine_flow_begin_request(fe_engine* engine, const float* condition, const float* noise,
+                                 const fe_condition_metadata* metadata);
+
+/* engine.h:344-348 — cancel tracked solves of a lower generation; safe to call from another
+ * thread while a solve advances.  The solve stops before its next step. */
+void fe_engine_cancel_before(fe_engine* engine, uint64_t generation);
+
+/* engine.h:350-363 — run at most `step_budget` solver steps; `action` [horizon][action_dim]
+ * receives the current state (the final x(1) once *steps_remaining is 0).  Status 6 when no
+ * flow solve is active, 8 after a cancellation (steps_remaining is still written). */
+int fe_engine_flow_advance(fe_engine* engine, size_t step_budget, float* action,
+                           size_t* steps_remaining);
+
+/* engine.h:365-366 — metadata of the current action of the engine's resumable solve. */
+int fe_engine_flow_action_metadata(const fe_engine* engine, fe_action_metadata* metadata);
+
 /* engine.h:395 */
 void fe_engine_free(fe_engine* engine);
 
@@ -188,6 +255,30 @@ int fe_engine_sample_condition_batch(fe_engine* engine, const float* condition,
 int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
                                       const float* normalized_sample, size_t batch,
                                       float timestep, float* predicted_noise);
+
+/* Resumable DDIM/DDPM solve, the Diffusion Policy counterpart of fe_engine_flow_begin /
+ * fe_engine_flow_advance with the same rules (one solve per engine, ended by other sampling
+ * calls).  After k of n steps `action` holds the current sample x_t in action units; after all n
+ * it equals fe_engine_sample_diffusion's action with the same inputs, bit for bit.  Status 6
+ * when no diffusion solve is active.  fe_engine_flow_action_metadata describes this solve too
+ * (`solver` = scheduler, remaining_nfe = remaining steps). */
+int fe_engine_diffusion_begin(fe_engine* engine, const float* condition, const float* noise,
+                              size_t steps, int scheduler, uint64_t seed);
+
+/* As fe_engine_diffusion_begin, but cancellable: `generation` is tracked as
+ * fe_engine_flow_begin_request tracks it, and fe_engine_cancel_before with a higher generation
+ * stops the solve before its next step (fe_engine_diffusion_advance then returns 8). */
+int fe_engine_diffusion_begin_generation(fe_engine* engine, const float* condition,
+                                         const float* noise, size_t steps, int scheduler,
+                                         uint64_t seed, uint64_t generation);
+
+int fe_engine_diffusion_advance(fe_engine* engine, size_t step_budget, float* action,
+                                size_t* steps_remaining);
+
+/* The model digest that fe_engine_model_metadata reports for engines created from these
+ * weights (the reference's tensor fingerprint, protocol/model_identity.cc:124-148); needs no
+ * GPU, so a host process can check request metadata against a checkpoint. */
+int fe_weights_model_digest(const fe_weights* weights, fe_model_digest* digest);
 
 /* Device-resident variants: the pointers are device memory (hipMalloc) of the same shapes;
  * nothing crosses PCIe.  `kind` 0 = DDIM/DDPM (`mode` = scheduler, `seed` used by DDPM),

@@ -18,6 +18,10 @@ Parity pins for each oracle function (the tests that fix it):
   DDIM / DDPM ............... closed-form update on a mocked eps, clip invariant (actions inside
                               [min, max]), seed independence (DDIM) and seed dependence (DDPM)
   flow ODE .................. Euler/RK4 on a zeroed velocity network (constant v = bias)
+  partial samples ........... closed form after k of n steps on a constant epsilon / velocity
+                              (fixes the timestep of each step); k = n equals the whole sample
+  model fingerprint ......... fingerprint.py: XXH64 from the independent xxhash package; the
+                              composition is restated and checked by its sensitivity invariants
 """
 
 from __future__ import annotations
@@ -61,6 +65,10 @@ def lib():
                                  ctypes.c_uint64, _f32p]
         L.dpo_sample_flow.argtypes = [ctypes.c_void_p, _f32p, _f32p, ctypes.c_size_t,
                                       ctypes.c_int, _f32p]
+        L.dpo_sample_partial.argtypes = [ctypes.c_void_p, _f32p, _f32p, ctypes.c_size_t,
+                                         ctypes.c_int, ctypes.c_uint64, ctypes.c_size_t, _f32p]
+        L.dpo_sample_flow_partial.argtypes = [ctypes.c_void_p, _f32p, _f32p, ctypes.c_size_t,
+                                              ctypes.c_int, ctypes.c_size_t, _f32p]
         L.dpo_sample_batch.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _f32p, _f32p,
                                        ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_uint64, _f32p, ctypes.c_uint]
@@ -132,6 +140,27 @@ class Oracle:
         rc = lib().dpo_sample(self._h, _p(cond), _p(noise), steps, scheduler, seed, _p(out))
         if rc:
             raise RuntimeError(f"oracle sample failed ({rc})")
+        return out.reshape(self.horizon, self.action_dim)
+
+    def sample_partial(self, cond, noise, steps: int, done: int, scheduler: int = 0,
+                       seed: int = 0) -> np.ndarray:
+        """The first `done` of `steps` DDIM/DDPM steps; the sample in action units."""
+        cond, noise = _f(cond), _f(noise)
+        out = np.empty(self.values, np.float32)
+        rc = lib().dpo_sample_partial(self._h, _p(cond), _p(noise), steps, scheduler, seed, done,
+                                      _p(out))
+        if rc:
+            raise RuntimeError(f"oracle partial sample failed ({rc})")
+        return out.reshape(self.horizon, self.action_dim)
+
+    def sample_flow_partial(self, cond, x0, steps: int, method: int, done: int) -> np.ndarray:
+        """The first `done` of `steps` ODE steps."""
+        cond, x0 = _f(cond), _f(x0)
+        out = np.empty(self.values, np.float32)
+        rc = lib().dpo_sample_flow_partial(self._h, _p(cond), _p(x0), steps, method, done,
+                                           _p(out))
+        if rc:
+            raise RuntimeError(f"oracle partial flow sample failed ({rc})")
         return out.reshape(self.horizon, self.action_dim)
 
     def sample_flow(self, cond, x0, steps: int, method: int) -> np.ndarray:

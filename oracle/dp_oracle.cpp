@@ -753,13 +753,15 @@ struct Model {
   }
 
   // diffusion.cc:979-1034 (host path).
+  // `done` < steps stops after that many steps and returns the current sample in action units
+  // (the state a resumable solve exposes between steps).
   void sample(const float* condv, const float* noise, std::size_t steps, int scheduler,
-              std::uint64_t seed, float* action) {
+              std::uint64_t seed, float* action, std::size_t done) {
     const std::size_t n = A * H;
     std::vector<float> x(noise, noise + n), e(n);
     Gaussian gaussian(seed);
     const std::size_t ratio = T / steps;
-    for (std::size_t i = 0; i < steps; ++i) {
+    for (std::size_t i = 0; i < std::min(done, steps); ++i) {
       const std::size_t ts = (steps - 1 - i) * ratio;
       const std::ptrdiff_t prev = static_cast<std::ptrdiff_t>(ts) - static_cast<std::ptrdiff_t>(ratio);
       denoise(condv, x.data(), static_cast<float>(ts), e.data());
@@ -794,11 +796,13 @@ struct Model {
   }
 
   // Flow-head ODE update (flow.cc:291-318, span_ops.h:27-52) with the U-Net as the velocity.
-  void sample_flow(const float* condv, const float* x0, std::size_t steps, int method, float* out) {
+  // `done` < steps stops after that many ODE steps (flow.cc:260-318 advanced in bounded units).
+  void sample_flow(const float* condv, const float* x0, std::size_t steps, int method, float* out,
+                   std::size_t done) {
     const std::size_t n = A * H;
     std::vector<float> x(x0, x0 + n), k1(n), k2(n), k3(n), k4(n), probe(n);
     const float dt = 1.0f / static_cast<float>(steps);
-    for (std::size_t s = 0; s < steps; ++s) {
+    for (std::size_t s = 0; s < std::min(done, steps); ++s) {
       const float t = static_cast<float>(s) * dt;
       denoise(condv, x.data(), t, k1.data());
       if (method == 0) {
@@ -898,7 +902,29 @@ int dpo_sample(void* handle, const float* cond, const float* noise, std::size_t 
   if (!h || !cond || !noise || !action || steps == 0 || steps > h->model.T) return 1;
   if (scheduler != 0 && scheduler != 1) return 5;
   if (h->model.pred != 0) return 4;
-  h->model.sample(cond, noise, steps, scheduler, seed, action);
+  h->model.sample(cond, noise, steps, scheduler, seed, action, steps);
+  return 0;
+}
+
+// The first `done` steps of dpo_sample / dpo_sample_flow (done <= steps).
+int dpo_sample_partial(void* handle, const float* cond, const float* noise, std::size_t steps,
+                       int scheduler, std::uint64_t seed, std::size_t done, float* action) {
+  auto* h = static_cast<Handle*>(handle);
+  if (!h || !cond || !noise || !action || steps == 0 || steps > h->model.T || done > steps)
+    return 1;
+  if (scheduler != 0 && scheduler != 1) return 5;
+  if (h->model.pred != 0) return 4;
+  h->model.sample(cond, noise, steps, scheduler, seed, action, done);
+  return 0;
+}
+
+int dpo_sample_flow_partial(void* handle, const float* cond, const float* x0, std::size_t steps,
+                            int method, std::size_t done, float* out) {
+  auto* h = static_cast<Handle*>(handle);
+  if (!h || !cond || !x0 || !out || steps == 0 || done > steps) return 1;
+  if (method < 0 || method > 2) return 5;
+  if (h->model.pred != 1) return 4;
+  h->model.sample_flow(cond, x0, steps, method, out, done);
   return 0;
 }
 
@@ -908,7 +934,7 @@ int dpo_sample_flow(void* handle, const float* cond, const float* x0, std::size_
   if (!h || !cond || !x0 || !out || steps == 0) return 1;
   if (method < 0 || method > 2) return 5;
   if (h->model.pred != 1) return 4;
-  h->model.sample_flow(cond, x0, steps, method, out);
+  h->model.sample_flow(cond, x0, steps, method, out, steps);
   return 0;
 }
 
@@ -927,9 +953,9 @@ int dpo_sample_batch(void* handle, std::size_t batch, const float* cond, const f
   auto worker = [&]() {
     for (std::size_t b = next.fetch_add(1); b < batch; b = next.fetch_add(1)) {
       if (kind == 0)
-        m.sample(cond + b * m.cond, noise + b * n, steps, mode, seed, out + b * n);
+        m.sample(cond + b * m.cond, noise + b * n, steps, mode, seed, out + b * n, steps);
       else
-        m.sample_flow(cond + b * m.cond, noise + b * n, steps, mode, out + b * n);
+        m.sample_flow(cond + b * m.cond, noise + b * n, steps, mode, out + b * n, steps);
     }
   };
   std::vector<std::thread> th;

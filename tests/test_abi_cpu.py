@@ -110,3 +110,94 @@ def test_invalid_meta_rejected_before_device(tmp_path):
     ck.write_safetensors(p, tensors.items())
     with pytest.raises(RuntimeError, match="dp.meta"):
         flowedge_amd.Engine(p)
+
+
+def test_resumable_entry_points_validate_without_engine():
+    lib = flowedge_amd.lib()
+    out = (ctypes.c_float * 4)()
+    rem = ctypes.c_size_t(77)
+    assert lib.fe_engine_flow_begin(None, None, None, 10, 0) == 1
+    assert flowedge_amd.last_error() == "Invalid arguments to fe_engine_flow_begin"
+    assert lib.fe_engine_flow_advance(None, 1, out, ctypes.byref(rem)) == 1
+    assert flowedge_amd.last_error() == "Invalid arguments to fe_engine_flow_advance"
+    assert rem.value == 77  # not written on argument errors (engine.cc:689-692)
+    assert lib.fe_engine_diffusion_begin(None, None, None, 10, 0, 0) == 1
+    assert lib.fe_engine_diffusion_begin_generation(None, None, None, 10, 0, 0, 1) == 1
+    assert lib.fe_engine_diffusion_advance(None, 1, out, None) == 1
+    md = flowedge_amd.ConditionMetadata()
+    assert lib.fe_engine_make_condition_metadata(None, 0, 0, 0, 10, 0, ctypes.byref(md)) == 1
+    assert lib.fe_engine_flow_begin_request(None, None, None, ctypes.byref(md)) == 1
+    assert flowedge_amd.last_error() == "Invalid versioned flow request metadata"
+    amd = flowedge_amd.ActionMetadata()
+    assert lib.fe_engine_flow_action_metadata(None, ctypes.byref(amd)) == 1
+    lib.fe_engine_cancel_before(None, 5)  # no-op on a null engine
+    # protocol/contracts.h:139-142 layouts.
+    assert ctypes.sizeof(md) == 88 and ctypes.sizeof(amd) == 80
+    assert ctypes.sizeof(flowedge_amd.ModelMetadata) == 96
+
+
+def test_weights_digest_matches_reference_fingerprint(tmp_path):
+    from oracle import fingerprint
+    path = ck.write_synthetic(str(tmp_path / "tiny.safetensors"), ck.SPECS["tiny"])
+    digest = flowedge_amd.weights_digest(path)
+    assert digest == fingerprint.fingerprint(path)
+    assert digest == flowedge_amd.weights_digest(path)  # deterministic
+
+
+def _write_raw_safetensors(path, entries, metadata=True):
+    """entries: (name, dtype, shape, raw bytes); writes them in the given order."""
+    import json
+    import struct
+    header, blobs, off = {}, [], 0
+    if metadata:
+        header["__metadata__"] = {"format": "pt"}
+    for name, dtype, shape, raw in entries:
+        header[name] = {"dtype": dtype, "shape": shape, "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    js = json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(js)) + js + b"".join(blobs))
+    return str(path)
+
+
+def test_fingerprint_covers_every_hash_branch_and_skips_other_dtypes(tmp_path):
+    # Names of 1..40 bytes and one over 127 (cut as the reference cuts it), contents of 2..70
+    # bytes (XXH64's short path, its 32-byte stripes and every tail), an I8 tensor and the
+    # __metadata__ entry that the loader skips.
+    from oracle import fingerprint
+    import numpy as np
+    rng = np.random.default_rng(3)
+    entries = []
+    for i in range(1, 36):
+        name = ("t%02d" % i + "x" * 40)[:i + 5] if i % 3 else "n" * i
+        entries.append((name, "BF16", [i], rng.integers(0, 2**16, i, dtype=np.uint16).tobytes()))
+    for i in range(1, 12):
+        entries.append((f"f{i}", "F32", [1, i], rng.standard_normal(i).astype(np.float32).tobytes()))
+    entries.append(("q" * 140, "F32", [2, 2, 2, 2], np.arange(16, dtype=np.float32).tobytes()))
+    entries.append(("skipped.int8", "I8", [3], b"\x01\x02\x03"))
+    p = _write_raw_safetensors(tmp_path / "branches.safetensors", entries)
+    assert flowedge_amd.weights_digest(p) == fingerprint.fingerprint(p)
+    without = _write_raw_safetensors(tmp_path / "no_int8.safetensors", entries[:-1],
+                                     metadata=False)
+    assert flowedge_amd.weights_digest(without) == flowedge_amd.weights_digest(p)
+
+
+def test_fingerprint_sensitivity(tmp_path):
+    # core_model_tests.cc:392-393: equal inputs give equal digests, any change another digest.
+    import numpy as np
+    a = np.arange(12, dtype=np.float32).tobytes()
+    base = [("w", "F32", [3, 4], a), ("b", "F32", [4], a[:16])]
+    variants = {
+        "base": base,
+        "content": [("w", "F32", [3, 4], a[:-1] + b"\x7f"), base[1]],
+        "name": [("W", "F32", [3, 4], a), base[1]],
+        "shape": [("w", "F32", [4, 3], a), base[1]],
+        "order": [base[1], base[0]],
+        "dtype": [("w", "BF16", [6, 4], a), base[1]],
+    }
+    digests = {k: flowedge_amd.weights_digest(_write_raw_safetensors(tmp_path / f"{k}.st", v))
+               for k, v in variants.items()}
+    assert len(set(digests.values())) == len(digests)
+    again = flowedge_amd.weights_digest(_write_raw_safetensors(tmp_path / "again.st", base))
+    assert again == digests["base"]

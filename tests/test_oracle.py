@@ -236,6 +236,49 @@ def test_zero_output_conv_gives_bias_and_closed_form_ddim(ckpt_dir):
     assert np.all(got >= -1.0) and np.all(got <= 1.0)
 
 
+def test_partial_sampling_closed_form(ckpt_dir):
+    # With a constant epsilon e the DDIM x0 prediction never changes after the first step
+    # (x_prev = sqrt(a_prev) x0 + sqrt(1 - a_prev) e re-predicts the same clip(x0)), so after k of
+    # n steps x_k = sqrt(a_p) clip(x0) + sqrt(1 - a_p) e with p = (n - 1 - k) * (T / n), and
+    # a_p = 1 once p < 0.  This fixes which timestep each step of a resumable solve uses.
+    spec = ck.SPECS["tiny"]
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, "tiny_zero_out.safetensors"), spec,
+                                  zero=("dp.f.o.w",))
+    o = oracle.Oracle(path)
+    e = ck.read_safetensors(path)["dp.f.o.b"].astype(np.float64)[None, :]
+    cond, noise = ck.inputs(spec)
+    ac = unet_ref.alphas_cumprod_f64(100)
+    for steps in (1, 4, 10):
+        ratio = 100 // steps
+        x = noise[0].astype(np.float64)
+        at = ac[(steps - 1) * ratio]
+        x0 = np.clip((x - np.sqrt(1 - at) * e) / np.sqrt(at), -1.0, 1.0)
+        for k in range(steps + 1):
+            got = o.sample_partial(cond[0], noise[0], steps, k, 0, 0)
+            if k == 0:
+                want = x  # action range [-1, 1]: unnormalisation is the identity
+            else:
+                p = (steps - 1 - k) * ratio
+                ap = ac[p] if p >= 0 else 1.0
+                want = np.sqrt(ap) * x0 + np.sqrt(1 - ap) * e
+            np.testing.assert_allclose(got, want, atol=2e-5, err_msg=f"steps={steps} k={k}")
+        assert np.array_equal(o.sample_partial(cond[0], noise[0], steps, steps, 1, 7),
+                              o.sample(cond[0], noise[0], steps, 1, 7))
+    # Flow: constant velocity v = bias gives x_k = x0 + (k / n) v for every solver.
+    fspec = ck.UNetSpec(dims=(64, 128, 256), action_dim=7, cond_dim=32, prediction=1)
+    fpath = unet_ref.write_variant(os.path.join(ckpt_dir, "flow_zero_out.safetensors"), fspec,
+                                   zero=("dp.f.o.w",))
+    fo = oracle.Oracle(fpath)
+    v = ck.read_safetensors(fpath)["dp.f.o.b"][None, :]
+    fc, fx = ck.inputs(fspec)
+    for method, steps in ((0, 5), (1, 3), (2, 4)):
+        for k in range(steps + 1):
+            got = fo.sample_flow_partial(fc[0], fx[0], steps, method, k)
+            np.testing.assert_allclose(got, fx[0] + (k / steps) * v, atol=3e-6)
+        assert np.array_equal(fo.sample_flow_partial(fc[0], fx[0], steps, method, steps),
+                              fo.sample_flow(fc[0], fx[0], steps, method))
+
+
 def test_flow_constant_velocity_is_exact(ckpt_dir):
     spec = ck.UNetSpec(dims=(64, 128, 256), action_dim=7, cond_dim=32, prediction=1)
     path = unet_ref.write_variant(os.path.join(ckpt_dir, "flow_zero_out.safetensors"), spec,
