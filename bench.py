@@ -334,6 +334,31 @@ def main():
         host.append((time.perf_counter() - t0) * 1e3)
     host_p50, host_p99 = percentile(host[5:], 50), percentile(host[5:], 99)
 
+    # Resumable DDIM-10 solve, one step per advance call (host pointers, engine.h:321-366).
+    out1 = np.empty((spec.horizon, spec.action_dim), np.float32)
+    begins, advances, solves = [], [], []
+    for i in range(25):
+        t0 = time.perf_counter()
+        eng.diffusion_begin(cond[0], noise[0], steps=steps_ddim)
+        t1 = time.perf_counter()
+        per = []
+        for _ in range(steps_ddim):
+            ta = time.perf_counter()
+            eng.diffusion_advance(out1, 1)
+            per.append((time.perf_counter() - ta) * 1e3)
+        if i >= 5:
+            begins.append((t1 - t0) * 1e3)
+            advances.extend(per)
+            solves.append((time.perf_counter() - t0) * 1e3)
+    resumable = {"begin_p50_ms": round(percentile(begins, 50), 4),
+                 "advance_1step_p50_ms": round(percentile(advances, 50), 4),
+                 "advance_1step_p99_ms": round(percentile(advances, 99), 4),
+                 "solve_p50_ms": round(percentile(solves, 50), 4),
+                 "definition": "host-to-host: begin uploads condition/noise; each advance runs "
+                               "one DDIM step and copies the current action back"}
+    print(f"[bench] resumable DDIM-10: begin {resumable['begin_p50_ms']:.3f} ms, advance(1) "
+          f"{resumable['advance_1step_p50_ms']:.3f} ms", file=sys.stderr, flush=True)
+
     # Parity of the timed path against the oracle is covered by tests; report the action norm.
     action = d_out.cpu().numpy()
 
@@ -407,6 +432,7 @@ def main():
         "host_to_host_p99_ms": round(host_p99, 4),
         "actions_per_sec_b1": round(spec.horizon / (p50 / 1e3), 1),
         "actions_per_sec_definition": "batch * horizon / p50 tick seconds",
+        "resumable_b1": resumable,
         "large_batch": large,
         "roofline": roof,
         "tick_roofline": {
