@@ -1,0 +1,68 @@
+// Shared pieces of the batched (matrix-core) convolution kernels: the implicit-GEMM argument
+// block, the input index of a tap, and the BF16-MFMA launcher (conv_mfma_bf16.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.h"
+
+namespace fe::hip::mm {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMmThreads = 256;
+
+// Column tiles: 64 output channels x 128 columns, or 64 x 64 when the larger column tile would
+// leave CUs without a workgroup.
+enum MmTile : int { kTile64x128 = 0, kTile64x64 = 1 };
+
+__host__ __device__ constexpr int lout_for(int mode, int lin) {
+  return mode == kConvSame ? lin : (mode == kConvDown ? lin / 2 : 2 * lin);
+}
+
+struct MmArgs {
+  const void* w;
+  const float* bias;
+  float* y;
+  std::int64_t ys;
+  const float* src;
+  std::int64_t src_stride;
+  int split;
+  const float* plain;
+  std::int64_t plain_stride;
+  int oc, ic, batch;
+  int mtiles, ntiles;
+  int ksplit;   // workgroups sharing one output tile's K range (1: no split)
+  float* part;  // ksplit > 1: partial tiles [ksplit][mtiles * ntiles][64 * NT]
+};
+
+// Input index read by output t through tap k, or -1 in the padding (t known only at run time).
+template <int MODE, int K, int LIN>
+__device__ __forceinline__ int src_at(int t, int k) {
+  if constexpr (MODE == kConvSame) {
+    const int j = t + k - K / 2;
+    return (j >= 0 && j < LIN) ? j : -1;
+  } else if constexpr (MODE == kConvDown) {
+    const int j = 2 * t + k - 1;
+    return (j >= 0 && j < LIN) ? j : -1;
+  } else {
+    const int num = t + 1 - k;  // ConvTranspose: output t = 2 * j + k - 1
+    if (num < 0 || (num & 1)) return -1;
+    const int j = num >> 1;
+    return j < LIN ? j : -1;
+  }
+}
+
+// BF16 matrix-core path for BF16 weights: the K loop walks 32 input channels per step.
+constexpr int kKCB = 32;
+
+// True when the BF16 kernels cover this convolution (BF16 weights, 32-channel multiples).
+bool mm_bf16_ok(const ConvOp& op, int split);
+
+// Launches the BF16 implicit GEMM for `a` (tiles and split as the F32 path plans them, with K
+// steps of kKCB channels).
+hipError_t launch_mm_bf16(const ConvOp& op, int tile, const MmArgs& a, hipStream_t s);
+
+}  // namespace fe::hip::mm

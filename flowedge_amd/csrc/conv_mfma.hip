@@ -22,6 +22,7 @@
 
 #include <cstdint>
 
+#include "conv_mfma.h"
 #include "device_common.h"
 #include "kernels.h"
 
@@ -30,48 +31,10 @@ namespace {
 
 using namespace dev;
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
+using namespace mm;
 
-constexpr int kMmThreads = 256;
 constexpr int kKC = 16;   // input channels per K step
 constexpr int kPad = 4;   // LDS row padding (floats)
-
-__host__ __device__ constexpr int lout_for(int mode, int lin) {
-  return mode == kConvSame ? lin : (mode == kConvDown ? lin / 2 : 2 * lin);
-}
-
-struct MmArgs {
-  const void* w;
-  const float* bias;
-  float* y;
-  std::int64_t ys;
-  const float* src;
-  std::int64_t src_stride;
-  int split;
-  const float* plain;
-  std::int64_t plain_stride;
-  int oc, ic, batch;
-  int mtiles, ntiles;
-  int ksplit;   // workgroups sharing one output tile's K range (1: no split)
-  float* part;  // ksplit > 1: partial tiles [ksplit][mtiles * ntiles][64 * NT]
-};
-
-// Input index read by output t through tap k, or -1 in the padding (t known only at run time).
-template <int MODE, int K, int LIN>
-__device__ __forceinline__ int src_at(int t, int k) {
-  if constexpr (MODE == kConvSame) {
-    const int j = t + k - K / 2;
-    return (j >= 0 && j < LIN) ? j : -1;
-  } else if constexpr (MODE == kConvDown) {
-    const int j = 2 * t + k - 1;
-    return (j >= 0 && j < LIN) ? j : -1;
-  } else {
-    const int num = t + 1 - k;  // ConvTranspose: output t = 2 * j + k - 1
-    if (num < 0 || (num & 1)) return -1;
-    const int j = num >> 1;
-    return j < LIN ? j : -1;
-  }
-}
 
 template <int MODE, int K, int LIN, int MT, int NT>
 struct MmShape {
@@ -395,10 +358,6 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
   }
 }
 
-// Tile configurations: 64 output channels x 128 columns, or 64 x 64 when the larger column tile
-// would leave CUs without a workgroup.
-enum MmTile : int { kTile64x128 = 0, kTile64x64 = 1 };
-
 template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
 hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
   using S = MmShape<MODE, K, LIN, MT, NT>;
@@ -483,7 +442,8 @@ bool conv_mfma_supported(const ConvOp& op, int split) {
 
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
-                     float* workspace, std::size_t workspace_floats, hipStream_t stream) {
+                     float* workspace, std::size_t workspace_floats, bool bf16_mma,
+                     hipStream_t stream) {
   if (!conv_mfma_supported(op, split) || batch <= 0) return hipErrorInvalidValue;
   if (split < op.ic && plain == nullptr) return hipErrorInvalidValue;
   MmArgs a{};
@@ -511,7 +471,8 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   // workgroups per CU, so that two K steps of weights stream per CU at a time.
   const int nt_cols = tile == kTile64x128 ? 128 : 64;
   const int tiles = a.mtiles * a.ntiles;
-  const int nsteps = (op.ic + kKC - 1) / kKC;
+  const bool use_bf16 = bf16_mma && mm_bf16_ok(op, split);
+  const int nsteps = use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
   a.ksplit = 1;
   if (tiles < 256 && workspace != nullptr) {
     int ks = (512 + tiles - 1) / tiles;
@@ -522,8 +483,9 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
       a.part = workspace;
     }
   }
-  const hipError_t st = op.bf16 ? by_kernel_mm<true>(op, tile, narrow, a, stream)
-                                : by_kernel_mm<false>(op, tile, narrow, a, stream);
+  const hipError_t st = use_bf16  ? launch_mm_bf16(op, tile, a, stream)
+                        : op.bf16 ? by_kernel_mm<true>(op, tile, narrow, a, stream)
+                                  : by_kernel_mm<false>(op, tile, narrow, a, stream);
   if (st != hipSuccess || a.ksplit == 1) return st;
   const std::int64_t elems = static_cast<std::int64_t>(tiles) * 64 * nt_cols;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((elems + kMmThreads - 1) / kMmThreads)),

@@ -256,6 +256,7 @@ struct FeEngine {
   std::size_t xnorm = 0;       // batched path: normalised input of one convolution [B][8192]
   std::size_t splitk = 0;      // batched path: split-K partial tiles (kSplitKFloats)
   std::size_t mfma_batch = 4;  // batches of at least this many samples use the matrix cores
+  bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
 
   std::list<GraphEntry> graphs;  // most recently used first
 
@@ -733,10 +734,10 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     }
     float* ws = e.ptr(e.splitk);
     FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws,
-                     kSplitKFloats, s));
+                     kSplitKFloats, e.bf16_mma, s));
     if (res != nullptr)
       FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws,
-                       kSplitKFloats, s));
+                       kSplitKFloats, e.bf16_mma, s));
     return hipSuccess;
   }
   return conv_fused(op, res, in, y, yr, batch, s);
@@ -1518,6 +1519,11 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   }
   e->max_batch = env_max_batch();
   e->mfma_batch = env_mfma_batch();
+  {
+    // FLOWEDGE_MFMA_BF16=0 keeps BF16 weights on the F32 matrix cores (widened, as F32 weights).
+    const char* v = std::getenv("FLOWEDGE_MFMA_BF16");
+    e->bf16_mma = !(v != nullptr && std::strcmp(v, "0") == 0);
+  }
   if (e->max_batch == 0) {
     set_error("FLOWEDGE_MAX_BATCH must be an integer from 1 through 65535");
     return nullptr;

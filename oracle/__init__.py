@@ -111,11 +111,15 @@ class Oracle:
         self.dims = tuple(int(d[i]) for i in range(self.stages))
 
     def close(self):
-        if self._h:
+        if getattr(self, "_h", None):
             lib().dpo_free(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may already be unloaded
+            pass
 
     @property
     def values(self) -> int:

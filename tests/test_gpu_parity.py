@@ -303,6 +303,28 @@ def test_bimanual_bf16_batched_mfma(ckpt_dir):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("bf16_mma", ["1", "0"])
+def test_bf16_weights_matrix_core_paths(ckpt_dir, monkeypatch, bf16_mma):
+    # BF16 weights at a batch on the matrix cores: the BF16 MFMA path (input split into two BF16
+    # terms, about 2^-17 relative per product) and the F32 MFMA path (weights widened).  Both are
+    # held to 1e-4 here; the contract bound for BF16-weight variants is 2e-2.
+    spec = ck.UNetSpec(dims=(64, 128, 256), horizon=8, action_dim=14, cond_dim=96,
+                       action_steps=4, bf16_weights=True)
+    path = ck.write_synthetic(os.path.join(ckpt_dir, "bf16_small.safetensors"), spec)
+    B = 8
+    cond, noise = ck.inputs(spec, batch=B)
+    o = oracle.Oracle(path)
+    monkeypatch.setenv("FLOWEDGE_MFMA_BF16", bf16_mma)
+    say(f"bf16 small batch={B} FLOWEDGE_MFMA_BF16={bf16_mma}")
+    with flowedge_amd.Engine(path) as e:
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+        again = e.sample_diffusion_batch(cond, noise, steps=10)
+    assert np.array_equal(got, again)  # fixed summation order: repeatable
+    err = maxerr(got, o.sample_batch(cond, noise, 10, workers=8))
+    say(f"bf16 small batch={B} max err {err:.3e}")
+    assert err <= TOL
+
+
 def test_flow_batched_mfma(ckpt_dir):
     spec = ck.SPECS["flow"]
     path = ck.cached_checkpoint("flow", ckpt_dir)
