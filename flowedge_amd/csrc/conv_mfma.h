@@ -55,14 +55,15 @@ __device__ __forceinline__ int src_at(int t, int k) {
   }
 }
 
-// BF16 matrix-core path for BF16 weights: the K loop walks 32 input channels per step.
+// BF16 matrix-core path: the K loop walks 32 input channels per step.
 constexpr int kKCB = 32;
 
-// True when the BF16 kernels cover this convolution (BF16 weights, 32-channel multiples).
+// True when the BF16 kernels cover this convolution's shape (32-channel multiples).
 bool mm_bf16_ok(const ConvOp& op, int split);
 
 // Launches the BF16 implicit GEMM for `a` (tiles and split as the F32 path plans them, with K
-// steps of kKCB channels).
+// steps of kKCB channels): two BF16 terms of the input against BF16 weights, or three products
+// of split input and split F32 weights.
 hipError_t launch_mm_bf16(const ConvOp& op, int tile, const MmArgs& a, hipStream_t s);
 
 }  // namespace fe::hip::mm

@@ -443,7 +443,7 @@ bool conv_mfma_supported(const ConvOp& op, int split) {
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
                      float* workspace, std::size_t workspace_floats, bool bf16_mma,
-                     hipStream_t stream) {
+                     bool f32_split, hipStream_t stream) {
   if (!conv_mfma_supported(op, split) || batch <= 0) return hipErrorInvalidValue;
   if (split < op.ic && plain == nullptr) return hipErrorInvalidValue;
   MmArgs a{};
@@ -471,7 +471,7 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   // workgroups per CU, so that two K steps of weights stream per CU at a time.
   const int nt_cols = tile == kTile64x128 ? 128 : 64;
   const int tiles = a.mtiles * a.ntiles;
-  const bool use_bf16 = bf16_mma && mm_bf16_ok(op, split);
+  const bool use_bf16 = (op.bf16 ? bf16_mma : f32_split) && mm_bf16_ok(op, split);
   const int nsteps = use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
   a.ksplit = 1;
   if (tiles < 256 && workspace != nullptr) {

@@ -257,6 +257,7 @@ struct FeEngine {
   std::size_t splitk = 0;      // batched path: split-K partial tiles (kSplitKFloats)
   std::size_t mfma_batch = 4;  // batches of at least this many samples use the matrix cores
   bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
+  bool f32_split = false;      // F32 weights on the BF16 matrix cores (split weights and input)
 
   std::list<GraphEntry> graphs;  // most recently used first
 
@@ -734,10 +735,10 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     }
     float* ws = e.ptr(e.splitk);
     FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws,
-                     kSplitKFloats, e.bf16_mma, s));
+                     kSplitKFloats, e.bf16_mma, e.f32_split, s));
     if (res != nullptr)
       FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws,
-                       kSplitKFloats, e.bf16_mma, s));
+                       kSplitKFloats, e.bf16_mma, e.f32_split, s));
     return hipSuccess;
   }
   return conv_fused(op, res, in, y, yr, batch, s);
@@ -1523,6 +1524,9 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     // FLOWEDGE_MFMA_BF16=0 keeps BF16 weights on the F32 matrix cores (widened, as F32 weights).
     const char* v = std::getenv("FLOWEDGE_MFMA_BF16");
     e->bf16_mma = !(v != nullptr && std::strcmp(v, "0") == 0);
+    // FLOWEDGE_MFMA_F32_SPLIT=1 runs F32 weights on the BF16 matrix cores as three split products.
+    v = std::getenv("FLOWEDGE_MFMA_F32_SPLIT");
+    e->f32_split = v != nullptr && std::strcmp(v, "1") == 0;
   }
   if (e->max_batch == 0) {
     set_error("FLOWEDGE_MAX_BATCH must be an integer from 1 through 65535");

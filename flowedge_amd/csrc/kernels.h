@@ -81,12 +81,14 @@ bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm);
 // workgroups whose partial tiles go to `workspace` (workspace_floats large enough) and are summed
 // by a second kernel in a fixed order.
 bool conv_mfma_supported(const ConvOp& op, int split);
-// BF16 weights (with 32-channel multiples) run on the BF16 matrix cores with the input split
-// into two BF16 terms when `bf16_mma` is set, on the F32 matrix cores otherwise.
+// Convolutions with 32-channel multiples can run on the BF16 matrix cores: BF16 weights against
+// the input split into two BF16 terms (`bf16_mma`), F32 weights as three products of split
+// weights and split input (`f32_split`).  Otherwise they run on the F32 matrix cores (BF16
+// weights widened).
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
                      float* workspace, std::size_t workspace_floats, bool bf16_mma,
-                     hipStream_t stream);
+                     bool f32_split, hipStream_t stream);
 
 // The prologue of a ConvInput with `norm` on its own: dst[b][0 : split*lin) =
 // mish(GN(src)) [* scale + shift] [+ res], per sample.

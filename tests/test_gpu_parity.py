@@ -275,6 +275,26 @@ def test_tiny_batched_mfma(tiny_engine, tiny_oracle):
                                                            scheduler="ddpm", seed=7)) <= 2 * TOL
 
 
+@pytest.mark.parametrize("workload", ["tiny", "pusht"])
+def test_f32_split_matrix_core_path(ckpt_dir, monkeypatch, workload):
+    # Opt-in F32 path on the BF16 matrix cores (three products of split weights and split input,
+    # about 1e-5 relative per layer): held to the fp32 bound 1e-4 (measured about 7e-5 at pusht
+    # size, which is why it is not the default).
+    spec = ck.SPECS[workload]
+    path = ck.cached_checkpoint(workload, ckpt_dir)
+    B = 19 if workload == "tiny" else 16
+    cond, noise = ck.inputs(spec, batch=B)
+    o = oracle.Oracle(path, threads=0)
+    monkeypatch.setenv("FLOWEDGE_MFMA_F32_SPLIT", "1")
+    say(f"{workload} DDIM-10 batch={B} FLOWEDGE_MFMA_F32_SPLIT=1")
+    with flowedge_amd.Engine(path) as e:
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+        assert np.array_equal(got, e.sample_diffusion_batch(cond, noise, steps=10))
+    err = maxerr(got, o.sample_batch(cond, noise, 10, workers=8))
+    say(f"{workload} split batch={B} max err {err:.3e}")
+    assert err <= TOL
+
+
 def test_pusht_batched_mfma(pusht):
     spec = ck.SPECS["pusht"]
     B = 16
