@@ -36,6 +36,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # dense
 METRIC = "p50 tick latency (B=1, 10-step DDIM) + actions/sec at B=256, % roofline"
 
 
@@ -198,12 +199,19 @@ def extra_configs(iters: int = 10):
         nfe = steps * per_step
         gbs = wbytes * nfe / (ms * 1e-3) / 1e9
         tflops = nfe_flops * batch * nfe / (ms * 1e-3) / 1e12
-        rows.append({"config": label, "device_p50_ms": round(ms, 3), "nfe": nfe,
-                     "actions_per_sec": round(batch * spec.horizon / (ms * 1e-3), 1),
-                     "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "tflops": round(tflops, 2),
-                     "fp32_mfma_frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "finite": bool(torch.isfinite(do).all().item())})
+        row = {"config": label, "device_p50_ms": round(ms, 3), "nfe": nfe,
+               "actions_per_sec": round(batch * spec.horizon / (ms * 1e-3), 1),
+               "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+               "tflops": round(tflops, 2), "finite": bool(torch.isfinite(do).all().item())}
+        if batch >= 4 and spec.bf16_weights:
+            # BF16 weights on the BF16 matrix cores, input split in two terms: two MFMA
+            # products per useful product.
+            row["mfma"] = "bf16 (2 products per multiply)"
+            row["mfma_frac"] = round(2 * tflops / BF16_MFMA_PEAK_TFLOPS, 4)
+        elif batch >= 4:
+            row["mfma"] = "fp32"
+            row["mfma_frac"] = round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)
+        rows.append(row)
         print(f"[bench] {label}: {ms:.3f} ms  ({gbs:.0f} GB/s weights, {tflops:.1f} TFLOP/s)",
               file=sys.stderr, flush=True)
     for e in engines.values():
