@@ -36,6 +36,9 @@ struct MmArgs {
   int mtiles, ntiles;
   int ksplit;   // workgroups sharing one output tile's K range (1: no split)
   float* part;  // ksplit > 1: partial tiles [ksplit][mtiles * ntiles][64 * NT]
+  // Byte sizes of the weight tensor and the batch of `src` / `plain` (buffer ranges of the BF16
+  // kernels; each below 2 GiB).
+  unsigned wbytes, srcbytes, plainbytes;
 };
 
 // Input index read by output t through tap k, or -1 in the padding (t known only at run time).

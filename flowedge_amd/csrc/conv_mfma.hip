@@ -471,7 +471,17 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   // workgroups per CU, so that two K steps of weights stream per CU at a time.
   const int nt_cols = tile == kTile64x128 ? 128 : 64;
   const int tiles = a.mtiles * a.ntiles;
-  const bool use_bf16 = (op.bf16 ? bf16_mma : f32_split) && mm_bf16_ok(op, split);
+  // The BF16 kernels address weights and inputs through 32-bit buffer offsets.
+  const std::uint64_t wb = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
+  const std::uint64_t sb = static_cast<std::uint64_t>(batch) * src_stride * 4;
+  const std::uint64_t pb =
+      plain != nullptr ? static_cast<std::uint64_t>(batch) * plain_stride * 4 : 0;
+  const bool ranges_fit = wb < (1ull << 31) && sb < (1ull << 31) && pb < (1ull << 31);
+  const bool use_bf16 =
+      (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
+  a.wbytes = static_cast<unsigned>(wb);
+  a.srcbytes = static_cast<unsigned>(sb);
+  a.plainbytes = static_cast<unsigned>(pb);
   const int nsteps = use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
   a.ksplit = 1;
   if (tiles < 256 && workspace != nullptr) {

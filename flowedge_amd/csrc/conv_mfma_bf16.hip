@@ -27,8 +27,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kPadB = 8;  // LDS row padding (BF16 values)
 
+// Workgroup shape per column tile: 64 x 128 blocks take eight wavefronts (two per SIMD, so one
+// wavefront's LDS reads and staging overlap another's MFMAs) in a 2 x 4 grid of 32 x 32 tiles;
+// 64 x 64 blocks take four wavefronts in a 2 x 2 grid (32 x 16 tiles would need one LDS read per
+// MFMA).
+__host__ __device__ constexpr int threads_for(int nt) { return nt >= 128 ? 512 : 256; }
+constexpr int kWaveRows = 2;
+
 template <int MODE, int K, int LIN, int MT, int NT, bool WF32>
 struct BShape {
+  static constexpr int kBThreads = threads_for(NT);
+  static constexpr int kWaveCols = kBThreads / 64 / kWaveRows;
   static constexpr int LOUT = lout_for(MODE, LIN);
   static constexpr int SB = NT / LOUT;            // samples per column tile
   static constexpr int WROW = K * kKCB + kPadB;   // LDS BF16 values per weight row
@@ -38,19 +47,27 @@ struct BShape {
   static constexpr int WVALS = MT * WROW;
   static constexpr int XVALS = XROWS * XROW;
   // 16-byte weight units per lane per step: 8 BF16 values, or 4 F32 values.
-  static constexpr int UW = MT * K * (kKCB / (WF32 ? 4 : 8)) / kMmThreads;
+  static constexpr int WUNITS = MT * K * (kKCB / (WF32 ? 4 : 8));  // weight units per step
+  static constexpr int UW = (WUNITS + kBThreads - 1) / kBThreads;
   static constexpr int WARR = WF32 ? 2 : 1;  // weight arrays in LDS (hi, lo)
-  static constexpr int XELEMS = SB * kKCB * LIN;               // input floats per step
-  static constexpr int XV = LIN >= 4 ? 4 : 1;
-  static constexpr int XUNITS = XELEMS / XV;
-  static constexpr int UX = (XUNITS + kMmThreads - 1) / kMmThreads;
-  static constexpr int WM = MT / 2, WN = NT / 2;
+  static constexpr int XP = LIN >= 4 ? 4 : LIN;   // positions per input load
+  static constexpr int NTQ = LIN / XP;              // position groups per sample
+  static constexpr int XUNITS8 = SB * NTQ * 4;      // input units (8 channels x XP positions)
+  static constexpr int WM = MT / kWaveRows, WN = NT / kWaveCols;
   static constexpr int TI = WM / 16, TJ = WN / 16;
   static constexpr std::size_t LDS_BYTES = (2 * WARR * WVALS + 4 * XVALS) * 2;
-  static_assert(MT * K * (kKCB / (WF32 ? 4 : 8)) % kMmThreads == 0, "weight units per lane");
-  static_assert(NT % LOUT == 0 && XELEMS % XV == 0, "column tile");
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wavefront tiles of 16 x 16 MFMA blocks");
+  static_assert(NT % LOUT == 0, "column tile");
+  static constexpr int UXN = (XUNITS8 + kBThreads - 1) / kBThreads;  // input units per lane
   static_assert(WROW % 8 == 0 && XROW % 8 == 0, "16-byte LDS rows");
 };
+
+constexpr unsigned kOutOfRange = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, kRsrcWord3);
+}
 
 __device__ __forceinline__ unsigned short bf16_bits(float v) {
   return __builtin_bit_cast(unsigned short, static_cast<__bf16>(v));
@@ -64,8 +81,9 @@ __device__ __forceinline__ void split_bf16(float v, unsigned short& hi, unsigned
 }
 
 template <int MODE, int K, int LIN, int MT, int NT, bool WF32>
-__global__ __launch_bounds__(kMmThreads) void conv_mfma_bf16_kernel(MmArgs a) {
+__global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs a) {
   using S = BShape<MODE, K, LIN, MT, NT, WF32>;
+  constexpr int kBThreads = S::kBThreads, kWaveCols = S::kWaveCols;
   extern __shared__ uint4 lds_b[];
   unsigned short* Ws = reinterpret_cast<unsigned short*>(lds_b);  // [2][WVALS] (hi)
   unsigned short* Wl = Ws + 2 * S::WVALS;                          // [2][WVALS] (lo, F32 weights)
@@ -93,102 +111,133 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_bf16_kernel(MmArgs a) {
     Xl[buf * S::XVALS + S::ZERO * S::XROW + c] = 0;
   }
 
-  constexpr int QPT = kKCB / (WF32 ? 4 : 8);  // 16-byte units per (row, tap)
+  // Staging.  Every global read is a buffer load whose per-lane byte offset is fixed for the
+  // whole K loop (computed once below); a wave-uniform scalar offset walks the K steps, and lanes
+  // with nothing to read get an out-of-range offset, which returns zeros without a branch.
+  constexpr int QPT = kKCB / (WF32 ? 4 : 8);  // 16-byte weight units per (row, tap)
   constexpr int QW = WF32 ? 4 : 8;             // weights per unit
-  uint4 wreg[S::UW];
-  float4 xreg[S::XV == 4 ? S::UX : 1];
-  float xs1[S::XV == 1 ? S::UX : 1];
-  auto load_step = [&](int step) {
-    const int ic0 = step * kKCB;
+  constexpr unsigned ES = WF32 ? 4u : 2u;      // weight element size
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(a.w, a.wbytes);
+  unsigned wvoff[S::UW];
+  int wlds[S::UW];
 #pragma unroll
-    for (int r = 0; r < S::UW; ++r) {
-      const int u = tid + r * kMmThreads;
-      const int m = u / (K * QPT), rem = u - m * (K * QPT);
-      const int k = rem / QPT, q = rem - k * QPT;
-      const int oc = m0 + m;
-      const std::int64_t idx = (static_cast<std::int64_t>(oc) * K + k) * a.ic + ic0 + QW * q;
-      wreg[r] = uint4{0u, 0u, 0u, 0u};
-      if (oc < a.oc) {
-        if constexpr (WF32)
-          wreg[r] = *reinterpret_cast<const uint4*>(static_cast<const float*>(a.w) + idx);
-        else
-          wreg[r] = *reinterpret_cast<const uint4*>(static_cast<const unsigned short*>(a.w) + idx);
-      }
+  for (int r = 0; r < S::UW; ++r) {
+    const int uu = tid + r * kBThreads;
+    const bool act = uu < S::WUNITS;
+    const int u = act ? uu : 0;
+    const int m = u / (K * QPT), rem = u - m * (K * QPT);
+    const int k = rem / QPT, q = rem - k * QPT;
+    const int oc = m0 + m;
+    wvoff[r] = act && oc < a.oc ? static_cast<unsigned>((oc * K + k) * a.ic + QW * q) * ES
+                                : kOutOfRange;
+    wlds[r] = act ? m * S::WROW + k * kKCB + QW * q : -1;
+  }
+  // Input units: 8 channels x P positions of one sample (P = min(LIN, 4)), loaded as 8 vectors of
+  // P floats (channels are LIN floats apart) and stored as P rows of 8 BF16 values per term.
+  constexpr int P = S::XP;
+  int xlds[S::UXN];
+  unsigned xvs[S::UXN], xvp[S::UXN];
+#pragma unroll
+  for (int n = 0; n < S::UXN; ++n) {
+    const int uu = tid + n * kBThreads;
+    const bool act = uu < S::XUNITS8;
+    const int u = act ? uu : 0;
+    const int bl = u / (S::NTQ * 4), v = u - bl * (S::NTQ * 4);
+    const int tq = v / 4, cg = v - tq * 4;
+    const int b = b0 + bl;
+    xlds[n] = act ? (bl * LIN + tq * P) * S::XROW + 8 * cg : -1;
+    xvs[n] = kOutOfRange;
+    xvp[n] = kOutOfRange;
+    if (act && b < a.batch) {
+      xvs[n] = static_cast<unsigned>((b * a.src_stride + 8 * cg * LIN + tq * P) * 4);
+      if (a.plain != nullptr)
+        xvp[n] = static_cast<unsigned>((b * a.plain_stride + 8 * cg * LIN + tq * P) * 4);
     }
+  }
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(a.src, a.srcbytes);
+  const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(a.plain != nullptr ? a.plain : a.src,
+                                                 a.plain != nullptr ? a.plainbytes : a.srcbytes);
+  // One K step's staged data in registers.
+  struct Regs {
+    uint4 w[S::UW];
+    float x[S::UXN][8][P];
+  };
+  auto load_step = [&](int step, Regs& R) {
+    const int ic0 = step * kKCB;
+    const unsigned ws = static_cast<unsigned>(ic0) * ES;
 #pragma unroll
-    for (int r = 0; r < S::UX; ++r) {
-      const int u = tid + r * kMmThreads;
-      if constexpr (S::XV == 4) {
-        const int bl = u / (kKCB * LIN / 4), v = u - bl * (kKCB * LIN / 4);
-        const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
-        const int b = b0 + bl, c = ic0 + ch;
-        float4 val = float4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (u < S::XUNITS && b < a.batch) {
-          const float* p = c < a.split ? a.src + b * a.src_stride + static_cast<std::int64_t>(c) * LIN
-                                       : a.plain + b * a.plain_stride +
-                                             static_cast<std::int64_t>(c - a.split) * LIN;
-          val = *reinterpret_cast<const float4*>(p + t4);
+    for (int r = 0; r < S::UW; ++r)
+      R.w[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff[r], ws, 0));
+    const bool from_src = ic0 < a.split;
+    const __amdgpu_buffer_rsrc_t xrs = from_src ? srs : prs;
+    const unsigned xs0 = static_cast<unsigned>((from_src ? ic0 : ic0 - a.split) * LIN * 4);
+#pragma unroll
+    for (int n = 0; n < S::UXN; ++n) {
+      const unsigned xv = from_src ? xvs[n] : xvp[n];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const unsigned so = xs0 + static_cast<unsigned>(j * LIN * 4);
+        if constexpr (P == 4) {
+          const float4 v =
+              __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xv, so, 0));
+          R.x[n][j][0] = v.x;
+          R.x[n][j][1] = v.y;
+          R.x[n][j][2] = v.z;
+          R.x[n][j][3] = v.w;
+        } else if constexpr (P == 2) {
+          const float2 v =
+              __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(xrs, xv, so, 0));
+          R.x[n][j][0] = v.x;
+          R.x[n][j][1] = v.y;
+        } else {
+          R.x[n][j][0] =
+              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xv, so, 0));
         }
-        xreg[r] = val;
-      } else {
-        const int bl = u / (kKCB * LIN), v = u - bl * (kKCB * LIN);
-        const int ch = v / LIN, t = v - ch * LIN;
-        const int b = b0 + bl, c = ic0 + ch;
-        float val = 0.0f;
-        if (u < S::XUNITS && b < a.batch)
-          val = c < a.split ? a.src[b * a.src_stride + static_cast<std::int64_t>(c) * LIN + t]
-                            : a.plain[b * a.plain_stride + static_cast<std::int64_t>(c - a.split) * LIN + t];
-        xs1[r] = val;
       }
     }
   };
-  auto store_step = [&](int buf) {
+  auto store_step = [&](int buf, const Regs& R) {
     unsigned short* W = Ws + buf * S::WVALS;
-    unsigned short* H = Xh + buf * S::XVALS;
-    unsigned short* L = Xl + buf * S::XVALS;
 #pragma unroll
     for (int r = 0; r < S::UW; ++r) {
-      const int u = tid + r * kMmThreads;
-      const int m = u / (K * QPT), rem = u - m * (K * QPT);
-      const int k = rem / QPT, q = rem - k * QPT;
-      const int off = m * S::WROW + k * kKCB + QW * q;
+      if (S::WUNITS % kBThreads != 0 && wlds[r] < 0) continue;
       if constexpr (WF32) {
-        const float4 v = __builtin_bit_cast(float4, wreg[r]);
+        const float4 v = __builtin_bit_cast(float4, R.w[r]);
         unsigned short h[4], l[4];
         split_bf16(v.x, h[0], l[0]);
         split_bf16(v.y, h[1], l[1]);
         split_bf16(v.z, h[2], l[2]);
         split_bf16(v.w, h[3], l[3]);
-        *reinterpret_cast<uint2*>(W + off) =
+        *reinterpret_cast<uint2*>(W + wlds[r]) =
             uint2{h[0] | (static_cast<unsigned>(h[1]) << 16), h[2] | (static_cast<unsigned>(h[3]) << 16)};
-        *reinterpret_cast<uint2*>(Wl + buf * S::WVALS + off) =
+        *reinterpret_cast<uint2*>(Wl + buf * S::WVALS + wlds[r]) =
             uint2{l[0] | (static_cast<unsigned>(l[1]) << 16), l[2] | (static_cast<unsigned>(l[3]) << 16)};
       } else {
-        *reinterpret_cast<uint4*>(W + off) = wreg[r];
+        *reinterpret_cast<uint4*>(W + wlds[r]) = R.w[r];
       }
     }
 #pragma unroll
-    for (int r = 0; r < S::UX; ++r) {
-      const int u = tid + r * kMmThreads;
-      if (u >= S::XUNITS) continue;
-      if constexpr (S::XV == 4) {
-        const int bl = u / (kKCB * LIN / 4), v = u - bl * (kKCB * LIN / 4);
-        const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
-        const int row = (bl * LIN + t4) * S::XROW + ch;
-        const float vals[4] = {xreg[r].x, xreg[r].y, xreg[r].z, xreg[r].w};
+    for (int n = 0; n < S::UXN; ++n) {
+      if (xlds[n] < 0) continue;
+      unsigned short* H = Xh + buf * S::XVALS + xlds[n];
+      unsigned short* L = Xl + buf * S::XVALS + xlds[n];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) split_bf16(vals[e], H[row + e * S::XROW], L[row + e * S::XROW]);
-      } else {
-        const int bl = u / (kKCB * LIN), v = u - bl * (kKCB * LIN);
-        const int ch = v / LIN, t = v - ch * LIN;
-        const int row = (bl * LIN + t) * S::XROW + ch;
-        split_bf16(xs1[r], H[row], L[row]);
+      for (int p = 0; p < P; ++p) {
+        bf16x8 hv, lv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const __bf16 h = static_cast<__bf16>(R.x[n][j][p]);
+          hv[j] = h;
+          lv[j] = static_cast<__bf16>(R.x[n][j][p] - static_cast<float>(h));
+        }
+        *reinterpret_cast<uint4*>(H + p * S::XROW) = __builtin_bit_cast(uint4, hv);
+        *reinterpret_cast<uint4*>(L + p * S::XROW) = __builtin_bit_cast(uint4, lv);
       }
     }
   };
 
   // Per-lane input row of every (column tile j, tap k): fixed for the whole K loop.
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave / kWaveCols, wc = wave % kWaveCols;
   const int kq = lane >> 4, l16 = lane & 15;
   int xrow[S::TJ][K];
 #pragma unroll
@@ -209,12 +258,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_bf16_kernel(MmArgs a) {
 #pragma unroll
     for (int j = 0; j < S::TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  load_step(s0);
-  store_step(0);
-  __syncthreads();
-  for (int step = s0; step < s1; ++step) {
-    const int buf = (step - s0) & 1;
-    if (step + 1 < s1) load_step(step + 1);
+  auto compute = [&](int buf) {
     const unsigned short* W = Ws + buf * S::WVALS;
     const unsigned short* WL = Wl + buf * S::WVALS;
     const unsigned short* H = Xh + buf * S::XVALS;
@@ -245,7 +289,18 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_bf16_kernel(MmArgs a) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
         }
     }
-    if (step + 1 < s1) store_step(buf ^ 1);
+  };
+
+  // K loop: the next step's loads are in flight while the matrix cores work on the current one.
+  Regs rn;
+  load_step(s0, rn);
+  store_step(0, rn);
+  __syncthreads();
+  for (int step = s0; step < s1; ++step) {
+    const int buf = (step - s0) & 1;
+    if (step + 1 < s1) load_step(step + 1, rn);
+    compute(buf);
+    if (step + 1 < s1) store_step(buf ^ 1, rn);
     __syncthreads();
   }
 
@@ -291,7 +346,7 @@ hipError_t launch(const MmArgs& a, hipStream_t s) {
     if (st != hipSuccess) return st;
     raised = true;
   }
-  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles * a.ksplit), dim3(kMmThreads), S::LDS_BYTES, s,
+  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles * a.ksplit), dim3(S::kBThreads), S::LDS_BYTES, s,
                      a);
   return hipGetLastError();
 }
