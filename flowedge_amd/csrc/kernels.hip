@@ -185,6 +185,24 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
   const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
   const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
 
+  // Reads that do not depend on the statistics are issued first, so their latency overlaps the
+  // reduction: the output conv's weights for the first action group and the sampler state.
+  constexpr int XPL = (kMaxActions * H + kUpdThreads - 1) / kUpdThreads;  // state values per lane
+  float w0[AG][CPL];
+#pragma unroll
+  for (int aa = 0; aa < AG; ++aa)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = tid + i * kUpdThreads;
+      w0[aa][i] = c < C && aa < A ? op.wo[static_cast<std::int64_t>(aa) * C + c] : 0.0f;
+    }
+  float xs[XPL];
+#pragma unroll
+  for (int r = 0; r < XPL; ++r) {
+    const int i = tid + r * kUpdThreads;
+    xs[r] = op.kind != kUpdateDenoise && i < A * H ? op.x[sample + i] : 0.0f;
+  }
+
   float hv[CPL][H];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
@@ -257,7 +275,8 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
 #pragma unroll
         for (int aa = 0; aa < AG; ++aa) {
           const int a = a0 + aa;
-          const float w = a < A ? op.wo[static_cast<std::int64_t>(a) * C + c] : 0.0f;
+          const float w = a0 == 0 ? w0[aa][i]
+                                  : (a < A ? op.wo[static_cast<std::int64_t>(a) * C + c] : 0.0f);
 #pragma unroll
           for (int t = 0; t < H; ++t) p[aa * H + t] = fmaf(w, hv[i][t], p[aa * H + t]);
         }
@@ -276,16 +295,20 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
     __syncthreads();
   }
 
-  for (int i = tid; i < A * H; i += kUpdThreads) {
+#pragma unroll
+  for (int r = 0; r < XPL; ++r) {
+    const int i = tid + r * kUpdThreads;
+    if (i >= A * H) break;
     const int a = i / H, t = i % H;  // state layout [A][H]
     const float e = eps[a][t];
+    const float xv = xs[r];
     const std::int64_t si = sample + i;
     switch (op.kind) {
       case kUpdateDenoise:
         op.out[sample + static_cast<std::int64_t>(t) * A + a] = e;
         break;
       case kUpdateDDIM: {
-        float x0 = (op.x[si] - op.sqrt_bt * e) / op.sqrt_at;
+        float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
         if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
         const float nx = op.sqrt_ap * x0 + op.sqrt_1map * e;
         op.x[si] = nx;
@@ -293,9 +316,9 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
         break;
       }
       case kUpdateDDPM: {
-        float x0 = (op.x[si] - op.sqrt_bt * e) / op.sqrt_at;
+        float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
         if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
-        float nx = op.coef_x0 * x0 + op.coef_x * op.x[si];
+        float nx = op.coef_x0 * x0 + op.coef_x * xv;
         if (op.add_noise)
           nx += op.sigma *
                 stream_gaussian(*op.seed, op.noise_offset + static_cast<std::uint64_t>(t) * A + a);
@@ -304,7 +327,7 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
         break;
       }
       case kUpdateEuler: {
-        const float nx = op.x[si] + op.dt * e;
+        const float nx = xv + op.dt * e;
         op.x[si] = nx;
         op.xin[si] = nx;
         break;
@@ -312,12 +335,12 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
       case kUpdateStage: {
         const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
         op.kbuf[op.slot * plane + si] = e;
-        op.xin[si] = op.x[si] + op.dt * e;
+        op.xin[si] = xv + op.dt * e;
         break;
       }
       case kUpdateHeun: {
         const float k1 = op.kbuf[si];
-        const float nx = op.x[si] + 0.5f * op.dt * (k1 + e);
+        const float nx = xv + 0.5f * op.dt * (k1 + e);
         op.x[si] = nx;
         op.xin[si] = nx;
         break;
@@ -325,7 +348,7 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
       case kUpdateRK4: {
         const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
         const float k1 = op.kbuf[si], k2 = op.kbuf[plane + si], k3 = op.kbuf[2 * plane + si];
-        const float nx = op.x[si] + (op.dt / 6.0f) * (k1 + 2.0f * k2 + 2.0f * k3 + e);
+        const float nx = xv + (op.dt / 6.0f) * (k1 + 2.0f * k2 + 2.0f * k3 + e);
         op.x[si] = nx;
         op.xin[si] = nx;
         break;
