@@ -276,6 +276,9 @@ def main():
                     help="rounds over the dominant convolution's layers")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel loop and a 256 MiB calibration copy")
+    ap.add_argument("--breakdown", metavar="WORKLOAD:BATCH",
+                    help="only the per-shape convolution timing of one U-Net evaluation at that "
+                         "batch (diagnostics and profiling), as JSON")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -288,6 +291,20 @@ def main():
 
     import flowedge_amd
     from flowedge_amd import checkpoint as ck
+
+    if args.breakdown:
+        work, batch = args.breakdown.split(":")
+        eng = flowedge_amd.Engine(ck.cached_checkpoint(work))
+        rows = conv_breakdown(eng, batch=int(batch), iters=10)
+        for r in rows:
+            print(f"[bench] {work} B={batch} {r['shape']:36s} x{r['launches_per_nfe']} "
+                  f"{r['us_per_launch']:9.2f} us {r.get('tflops', 0):7.1f} TFLOP/s", file=sys.stderr,
+                  flush=True)
+        print(json.dumps({"breakdown": work, "batch": int(batch),
+                          "rows": [{k: v for k, v in r.items() if k != "indices"} for r in rows]}),
+              flush=True)
+        eng.close()
+        return
 
     spec = ck.SPECS[args.workload]
     path = ck.cached_checkpoint(args.workload)
