@@ -201,3 +201,23 @@ def test_fingerprint_sensitivity(tmp_path):
     assert len(set(digests.values())) == len(digests)
     again = flowedge_amd.weights_digest(_write_raw_safetensors(tmp_path / "again.st", base))
     assert again == digests["base"]
+
+
+def test_plain_c_caller_links_and_runs(tmp_path):
+    # A C99 program built against include/flowedge.h and linked with -lflowedge_amd, as a
+    # reference C caller would switch (examples/core/diffusion_sample.cc:26-50).
+    import shutil
+    import subprocess
+    from oracle import fingerprint
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc is not available")
+    lib_dir = os.path.join(ROOT, "flowedge_amd")
+    exe = str(tmp_path / "abi_consumer")
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic",
+                    "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "c", "abi_consumer.c"), "-L", lib_dir,
+                    "-lflowedge_amd", f"-Wl,-rpath,{lib_dir}", "-o", exe], check=True)
+    path = ck.write_synthetic(str(tmp_path / "tiny.safetensors"), ck.SPECS["tiny"])
+    out = subprocess.run([exe, path], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "ok " + fingerprint.fingerprint(path)
