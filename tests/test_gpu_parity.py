@@ -295,6 +295,25 @@ def test_f32_split_matrix_core_path(ckpt_dir, monkeypatch, workload):
     assert err <= TOL
 
 
+def test_tiny_large_batch(ckpt_dir, monkeypatch):
+    # A batch far above the bench sizes: large grids and per-sample offsets on the matrix-core
+    # path, against the oracle on a spread of samples.
+    spec = ck.SPECS["tiny"]
+    path = ck.cached_checkpoint("tiny", ckpt_dir)
+    B = 1000
+    monkeypatch.setenv("FLOWEDGE_MAX_BATCH", "1024")
+    cond, noise = ck.inputs(spec, batch=B)
+    o = oracle.Oracle(path)
+    say(f"tiny DDIM-10 batch={B}")
+    with flowedge_amd.Engine(path) as e:
+        assert e.max_batch == 1024
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+    idx = [0, 1, 255, 256, 511, 767, 998, 999]
+    want = o.sample_batch(cond[idx], noise[idx], 10, workers=8)
+    assert maxerr(got[idx], want) <= TOL
+    assert np.all(np.isfinite(got))
+
+
 def test_pusht_batched_mfma(pusht):
     spec = ck.SPECS["pusht"]
     B = 16
