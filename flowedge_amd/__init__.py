@@ -37,7 +37,7 @@ EXPORTS = [
     "fe_engine_flow_begin_request", "fe_engine_cancel_before", "fe_engine_flow_advance",
     "fe_engine_flow_action_metadata", "fe_engine_diffusion_begin",
     "fe_engine_diffusion_begin_generation", "fe_engine_diffusion_advance",
-    "fe_weights_model_digest",
+    "fe_weights_model_digest", "fe_engine_conv_path",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -132,6 +132,7 @@ def lib():
                                       ctypes.POINTER(u64)]
     L.fe_engine_time_convs.argtypes = [vp, ctypes.POINTER(sz), sz, sz, sz,
                                        ctypes.POINTER(ctypes.c_float)]
+    L.fe_engine_conv_path.argtypes = [vp, sz, sz, ctypes.POINTER(cint)]
     L.fe_engine_flow_begin.argtypes = [vp, _f32p, _f32p, sz, cint]
     L.fe_engine_make_condition_metadata.argtypes = [vp, u64, u64, u64, sz, cint,
                                                     ctypes.POINTER(ConditionMetadata)]
@@ -431,6 +432,20 @@ class Engine:
                                               ctypes.byref(sb)))
             out.append({"index": i, "name": buf.value.decode(), "weight_bytes": wb.value,
                         "sample_bytes": sb.value})
+        return out
+
+    def conv_paths(self, batch: int = 1) -> list[str]:
+        """Kernels each convolution of convolutions() runs on at `batch`: "fused"
+        (weight-streaming), "matrix" (matrix-core implicit GEMM) or "general" (general-shape)."""
+        L = lib()
+        n = ctypes.c_size_t()
+        self._check(L.fe_engine_conv_count(self._h, ctypes.byref(n)))
+        names = ("fused", "matrix", "general")
+        out = []
+        p = ctypes.c_int()
+        for i in range(n.value):
+            self._check(L.fe_engine_conv_path(self._h, i, batch, ctypes.byref(p)))
+            out.append(names[p.value])
         return out
 
     def time_convolutions(self, indices, batch: int = 1, iters: int = 100) -> float:

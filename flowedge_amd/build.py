@@ -15,7 +15,8 @@ ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libflowedge_amd.so")
 SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/conv_fused.hip",
            "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip",
-           "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/identity.cpp"]
+           "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/conv_general.hip",
+           "csrc/identity.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 

@@ -75,33 +75,45 @@ int prologue_of(const ConvInput& in) {
   return -1;
 }
 
+// Every condition conv_fused needs; `p` receives the launch plan.
+bool fused_plan(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr, int batch,
+                LaunchPlan& p) {
+  const bool res = res1x1 != nullptr;
+  if (!plan_conv(op, res, in.split, in.norm, p)) return false;
+  if (prologue_of(in) < 0) return false;
+  if (in.norm && (in.groups <= 0 || in.groups > kMaxGroups || in.split % in.groups != 0 ||
+                  (in.split / in.groups * op.lin) % 4 != 0))
+    return false;
+  if (in.split < op.ic && in.plain == nullptr) return false;
+  if (res && (res1x1->k != 1 || res1x1->ic != op.ic || res1x1->oc != op.oc || yr.p == nullptr))
+    return false;
+  if (batch <= 0 || batch > 65535) return false;
+  // Weight tensors are addressed with 32-bit buffer offsets (out-of-range marker at 2 GiB).
+  const std::uint64_t wbytes = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
+  const std::uint64_t rwbytes =
+      res ? static_cast<std::uint64_t>(op.oc) * op.ic * (res1x1->bf16 ? 2 : 4) : 0;
+  if (wbytes >= kOutOfRange || rwbytes >= kOutOfRange) return false;
+  if (res && p.vec == 4 && res1x1->bf16 != op.bf16) return false;
+  return true;
+}
+
 }  // namespace
 
-bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm) {
+bool conv_fused_supported(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr,
+                          int batch) {
   LaunchPlan p;
-  return plan_conv(op, res1x1, split, norm, p);
+  return fused_plan(op, res1x1, in, yr, batch, p);
 }
 
 hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
                       View yr, int batch, hipStream_t stream) {
   const bool res = res1x1 != nullptr;
   LaunchPlan p;
-  if (!plan_conv(op, res, in.split, in.norm, p)) return hipErrorInvalidValue;
+  if (!fused_plan(op, res1x1, in, yr, batch, p)) return hipErrorInvalidValue;
   const int pro = prologue_of(in);
-  if (pro < 0) return hipErrorInvalidValue;
-  if (in.norm && (in.groups <= 0 || in.groups > kMaxGroups || in.split % in.groups != 0 ||
-                  (in.split / in.groups * op.lin) % 4 != 0))
-    return hipErrorInvalidValue;
-  if (in.split < op.ic && in.plain == nullptr) return hipErrorInvalidValue;
-  if (res && (res1x1->k != 1 || res1x1->ic != op.ic || res1x1->oc != op.oc || yr.p == nullptr))
-    return hipErrorInvalidValue;
-  if (batch <= 0 || batch > 65535) return hipErrorInvalidValue;
-  // Weight tensors are addressed with 32-bit buffer offsets (out-of-range marker at 2 GiB).
   const std::uint64_t wbytes = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
   const std::uint64_t rwbytes =
       res ? static_cast<std::uint64_t>(op.oc) * op.ic * (res1x1->bf16 ? 2 : 4) : 0;
-  if (wbytes >= kOutOfRange || rwbytes >= kOutOfRange) return hipErrorInvalidValue;
-  if (res && p.vec == 4 && res1x1->bf16 != op.bf16) return hipErrorInvalidValue;
   Args a{};
   a.wbytes = static_cast<unsigned>(wbytes);
   a.rwbytes = static_cast<unsigned>(rwbytes);

@@ -505,16 +505,18 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
 
 hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,
                     hipStream_t stream) {
-  if (!in.norm || batch <= 0 || in.groups <= 0 || in.groups > 32 || in.split % in.groups != 0 ||
-      (in.split / in.groups * lin) % 4 != 0 || in.split * lin > kNaMaxFloats)
+  if (!in.norm || batch <= 0 || in.groups <= 0 || in.split % in.groups != 0)
     return hipErrorInvalidValue;
+  if (in.groups > 32 || (in.split / in.groups * lin) % 4 != 0 ||
+      static_cast<std::int64_t>(in.split) * lin > kNaMaxFloats)
+    return norm_act_general(in, lin, dst, dst_stride, batch, stream);
   switch (lin) {
     case 1: hipLaunchKernelGGL(norm_act_kernel<1>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
     case 2: hipLaunchKernelGGL(norm_act_kernel<2>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
     case 4: hipLaunchKernelGGL(norm_act_kernel<4>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
     case 8: hipLaunchKernelGGL(norm_act_kernel<8>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
     case 16: hipLaunchKernelGGL(norm_act_kernel<16>, dim3(batch), dim3(kNaThreads), 0, stream, in, dst, dst_stride); break;
-    default: return hipErrorInvalidValue;
+    default: return norm_act_general(in, lin, dst, dst_stride, batch, stream);
   }
   return hipGetLastError();
 }

@@ -54,7 +54,6 @@ bool env_flag(const char* name) {
 
 constexpr unsigned kMaxPoolThreads = 8;  // engine_runtime.h:39
 constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
-constexpr std::size_t kMaxNormFloats = 8192;  // width * length of any normalised activation
 constexpr std::size_t kSplitKFloats = 1024 * 64 * 128;  // split-K partials: <= 1024 tiles of 64 x 128
 constexpr std::size_t kFinalNormGroups = 8;  // diffusion.cc:28
 constexpr std::size_t kAlign = 256;
@@ -122,36 +121,20 @@ bool parse_config(const fe::Checkpoint& ck, Config& c, std::string& err) {
   return true;
 }
 
-// Device kernels are specialised for these shapes; anything else is rejected at load.
+// Limits of the device path beyond the reference's own validation (parse_config).  Shapes the
+// specialised kernels have no instance for run on the general kernels, so only sizes that no
+// kernel addresses are refused.
 bool supported_shape(const Config& c, std::string& err) {
-  if (c.kernel != 3 && c.kernel != 5) {
-    err = "Unsupported U-Net kernel size (3 and 5 are supported)";
+  if (5 * c.tdim * sizeof(float) > fe::hip::kMaxTimeMlpLds) {
+    err = "Unsupported timestep embedding width (at most 8192)";
     return false;
   }
-  const std::size_t h = c.horizon;
-  if (h > 16 || (h & (h - 1)) != 0) {
-    err = "Unsupported horizon (powers of two up to 16 are supported)";
-    return false;
-  }
-  if (c.groups > 32) {
-    err = "Unsupported GroupNorm group count (at most 32)";
-    return false;
-  }
-  for (std::size_t s = 0; s < c.stages; ++s) {
-    if (c.dims[s] % (4 * c.groups) != 0 || c.dims[s] > 4096) {
-      err = "Unsupported U-Net width (each width must be a multiple of 4 * groups, at most 4096)";
-      return false;
-    }
-    // A workgroup stages one sample's activation in LDS: width * length <= 8192 floats per stage
-    // (up-stage inputs, twice that, are the 64 KB maximum).
-    if (c.dims[s] * (h >> s) > 8192) {
-      err = "Unsupported U-Net size (width * length must be at most 8192 at every stage)";
-      return false;
-    }
-  }
-  if (!fe::hip::update_supported(static_cast<int>(c.dims[0]), static_cast<int>(kFinalNormGroups),
-                                 static_cast<int>(c.horizon), static_cast<int>(c.action_dim))) {
-    err = "Unsupported final layer shape";
+  // Widths, lengths and channel counts are kernel arguments of type int.
+  std::size_t widest = c.cond_dim;
+  for (std::size_t s = 0; s < c.stages; ++s) widest = std::max(widest, 2 * c.dims[s]);
+  if (widest > (std::size_t{1} << 24) || c.horizon > (std::size_t{1} << 24) ||
+      c.action_dim > (std::size_t{1} << 24) || c.kernel > 4095) {
+    err = "Unsupported U-Net size";
     return false;
   }
   return true;
@@ -509,7 +492,11 @@ struct Builder {
       for (int k = 0; k < 2; ++k) acts(e.up[u][k]);
     e.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
     e.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
-    e.xnorm = plan.take(B * kMaxNormFloats * 4);
+    // Largest normalised activation (width * length of any block output).
+    std::size_t norm_floats = 0;
+    for (std::size_t st = 0; st < c.stages; ++st)
+      norm_floats = std::max(norm_floats, c.dims[st] * (c.horizon >> st));
+    e.xnorm = plan.take(B * norm_floats * 4);
     e.splitk = plan.take(kSplitKFloats * 4);
     return true;
   }
@@ -674,6 +661,9 @@ void bind_all(FeEngine& e) {
 hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
                          const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
                          int batch, hipStream_t s);
+enum class ConvPath : int { kFused = 0, kMatrix = 1, kGeneral = 2 };
+ConvPath conv_path(const FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
+                   const fe::hip::ConvInput& in, fe::hip::View yr, int batch);
 
 // Launches one fused convolution; while recording, also keeps its arguments and algorithmic
 // bytes (each weight and bias once, each activation and per-channel parameter once per sample).
@@ -715,13 +705,48 @@ hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
   return dispatch_conv(e, op, res, in, y, yr, batch, s);
 }
 
+// Kernels a convolution runs on at this batch size: the fused weight-streaming kernels (few
+// samples), the matrix cores (many samples), or the general-shape kernels when neither has an
+// instance for the shape.
+ConvPath conv_path(const FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
+                   const fe::hip::ConvInput& in, fe::hip::View yr, int batch) {
+  using namespace fe::hip;
+  const bool plain_ok = in.split == op.ic || in.plain != nullptr;
+  const bool mm_ok = plain_ok && conv_mfma_supported(op, in.split) &&
+                     (res == nullptr || conv_mfma_supported(*res, in.split));
+  const bool fused_ok = conv_fused_supported(op, res, in, yr, batch);
+  if (mm_ok && (static_cast<std::size_t>(batch) >= e.mfma_batch || !fused_ok))
+    return ConvPath::kMatrix;
+  return fused_ok ? ConvPath::kFused : ConvPath::kGeneral;
+}
+
 // Runs one fused convolution on the kernels chosen for this batch size.
 hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
                          const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
                          int batch, hipStream_t s) {
   using namespace fe::hip;
-  if (static_cast<std::size_t>(batch) >= e.mfma_batch && conv_mfma_supported(op, in.split) &&
-      (res == nullptr || conv_mfma_supported(*res, in.split))) {
+  const ConvPath path = conv_path(e, op, res, in, yr, batch);
+  if (path == ConvPath::kGeneral) {
+    // General shapes: the prologue as its own pass, then the FP32 implicit GEMM.
+    const float* src = in.src;
+    std::int64_t ss = in.src_stride;
+    if (in.norm) {
+      float* dst = in.mat != nullptr ? in.mat : e.ptr(e.xnorm);
+      const std::int64_t ds =
+          in.mat != nullptr ? in.mat_stride : static_cast<std::int64_t>(in.split) * op.lin;
+      FE_TRY(norm_act(in, op.lin, dst, ds, batch, s));
+      src = dst;
+      ss = ds;
+    }
+    float* ws = e.ptr(e.splitk);
+    FE_TRY(conv_general(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws,
+                        kSplitKFloats, s));
+    if (res != nullptr)
+      FE_TRY(conv_general(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws,
+                          kSplitKFloats, s));
+    return hipSuccess;
+  }
+  if (path == ConvPath::kMatrix) {
     // Many samples: the prologue as its own pass, then implicit GEMMs on the matrix cores.
     const float* src = in.src;
     std::int64_t ss = in.src_stride;
@@ -2141,6 +2166,24 @@ int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name
   }
   if (weight_bytes != nullptr) *weight_bytes = r.weight_bytes;
   if (sample_bytes != nullptr) *sample_bytes = r.sample_bytes;
+  return FE_STATUS_OK;
+}
+
+int fe_engine_conv_path(fe_engine* engine, size_t index, size_t batch, int* path) {
+  clear_error();
+  if (engine == nullptr || path == nullptr || batch == 0 || batch > engine->max_batch) {
+    set_error("Invalid arguments to fe_engine_conv_path");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const int rc = ensure_conv_records(engine);
+  if (rc != FE_STATUS_OK) return rc;
+  if (index >= engine->conv_records.size()) {
+    set_error("Convolution index out of range");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const FeEngine::ConvRecord& r = engine->conv_records[index];
+  *path = static_cast<int>(conv_path(*engine, r.op, r.has_res ? &r.res : nullptr, r.in, r.yr,
+                                     static_cast<int>(batch)));
   return FE_STATUS_OK;
 }
 

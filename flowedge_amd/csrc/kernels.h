@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
 
 namespace fe::hip {
@@ -71,9 +72,9 @@ struct ConvInput {
 hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
                       View yr, int batch, hipStream_t stream);
 
-// Returns false when conv_fused has no kernel for this shape: `res1x1` with a fused projection,
-// `split` channels from the prologue source, `norm` with a GroupNorm prologue.
-bool conv_supported(const ConvOp& op, bool res1x1, int split, bool norm);
+// True when conv_fused has a kernel for this convolution, input and batch.
+bool conv_fused_supported(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr,
+                          int batch);
 
 // Batched path (matrix cores).  y = conv(x) + bias with x a plain tensor: channels [0, split)
 // from `src`, the rest from `plain`.  ic and split are multiples of 16, or split == ic (narrow
@@ -91,9 +92,22 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
                      bool f32_split, hipStream_t stream);
 
 // The prologue of a ConvInput with `norm` on its own: dst[b][0 : split*lin) =
-// mish(GN(src)) [* scale + shift] [+ res], per sample.
+// mish(GN(src)) [* scale + shift] [+ res], per sample.  Shapes outside the per-sample kernel's
+// instances (split * lin > 8192, more than 32 groups, groups of lengths not a multiple of 4) run
+// on norm_act_general.
 hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,
                     hipStream_t stream);
+
+// General-shape path (conv_general.hip): any kernel size, length and width the checkpoint format
+// admits, for convolutions neither conv_fused nor conv_mfma has an instance for.  y = conv(x) +
+// bias with x a plain tensor (channels [0, split) from `src`, the rest from `plain`); the
+// reduction is split over workgroups through `workspace` when the tiles leave CUs idle.
+hipError_t conv_general(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
+                        const float* plain, std::int64_t plain_stride, View y, int batch,
+                        float* workspace, std::size_t workspace_floats, hipStream_t stream);
+// The prologue with one workgroup per (sample, group): any width, length and group count.
+hipError_t norm_act_general(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride,
+                            int batch, hipStream_t stream);
 
 // Timestep of the n-th U-Net evaluation of a sampling call, derived on the device:
 //   kTimesSingle: t = t0
@@ -110,7 +124,9 @@ struct TimeSpec {
   int method = 0;  // flow: 0 Euler, 1 Heun, 2 RK4
 };
 
-// m[n][:] = mish(te2(mish(te1(emb(t_n)) + b1)) + b2) for n < count.
+// m[n][:] = mish(te2(mish(te1(emb(t_n)) + b1)) + b2) for n < count.  The embedding and hidden
+// layer (5 * tdim floats) live in LDS: tdim <= kMaxTimeMlpLds / 20.
+constexpr std::size_t kMaxTimeMlpLds = 160 * 1024;
 hipError_t time_mlp(const TimeSpec& times, int count, const float* w1, const float* b1,
                     const float* w2, const float* b2, int tdim, float* m, hipStream_t stream);
 
@@ -159,8 +175,10 @@ struct UpdateOp {
   int add_noise = 0;
   float dt = 0;
 };
+// One block per sample.  Shapes outside the fused kernel's instances (horizon not a power of two
+// up to 16, c0 > 1024, more than 64 actions or 32 groups) run on a general kernel (one wavefront
+// per output value), which accepts any c0 divisible by `groups` (at most 64 groups).
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
-bool update_supported(int c0, int groups, int horizon, int action_dim);
 
 // action[b][t][a] = (x[b][a][t] + 1) / 2 * (max - min) + min   (or a plain transpose when
 // amin == nullptr).

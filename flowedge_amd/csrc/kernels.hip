@@ -160,6 +160,66 @@ __device__ __forceinline__ float stream_gaussian(std::uint64_t seed, std::uint64
   return (n & 1) ? radius * sinf(angle) : radius * cosf(angle);
 }
 
+// The sampler update of state value (a, t) (state layout [A][H]) from the U-Net output e and
+// the current state xv (diffusion.cc:995-1024, flow.cc:291-318).
+__device__ __forceinline__ void apply_update(const UpdateOp& op, std::int64_t sample, int a, int t,
+                                             int A, int H, float e, float xv) {
+  const std::int64_t si = sample + static_cast<std::int64_t>(a) * H + t;
+  switch (op.kind) {
+    case kUpdateDenoise:
+      op.out[sample + static_cast<std::int64_t>(t) * A + a] = e;
+      break;
+    case kUpdateDDIM: {
+      float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
+      if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
+      const float nx = op.sqrt_ap * x0 + op.sqrt_1map * e;
+      op.x[si] = nx;
+      if (op.xin != op.x) op.xin[si] = nx;
+      break;
+    }
+    case kUpdateDDPM: {
+      float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
+      if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
+      float nx = op.coef_x0 * x0 + op.coef_x * xv;
+      if (op.add_noise)
+        nx += op.sigma *
+              stream_gaussian(*op.seed, op.noise_offset + static_cast<std::uint64_t>(t) * A + a);
+      op.x[si] = nx;
+      if (op.xin != op.x) op.xin[si] = nx;
+      break;
+    }
+    case kUpdateEuler: {
+      const float nx = xv + op.dt * e;
+      op.x[si] = nx;
+      op.xin[si] = nx;
+      break;
+    }
+    case kUpdateStage: {
+      const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
+      op.kbuf[op.slot * plane + si] = e;
+      op.xin[si] = xv + op.dt * e;
+      break;
+    }
+    case kUpdateHeun: {
+      const float k1 = op.kbuf[si];
+      const float nx = xv + 0.5f * op.dt * (k1 + e);
+      op.x[si] = nx;
+      op.xin[si] = nx;
+      break;
+    }
+    case kUpdateRK4: {
+      const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
+      const float k1 = op.kbuf[si], k2 = op.kbuf[plane + si], k3 = op.kbuf[2 * plane + si];
+      const float nx = xv + (op.dt / 6.0f) * (k1 + 2.0f * k2 + 2.0f * k3 + e);
+      op.x[si] = nx;
+      op.xin[si] = nx;
+      break;
+    }
+    default:
+      break;
+  }
+}
+
 constexpr int kUpdThreads = 512;
 constexpr int kMaxUpdateChannelsPerLane = 2;  // c0 <= 1024
 constexpr int kMaxUpdateGroups = 32;
@@ -299,62 +359,58 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
   for (int r = 0; r < XPL; ++r) {
     const int i = tid + r * kUpdThreads;
     if (i >= A * H) break;
-    const int a = i / H, t = i % H;  // state layout [A][H]
-    const float e = eps[a][t];
-    const float xv = xs[r];
-    const std::int64_t si = sample + i;
-    switch (op.kind) {
-      case kUpdateDenoise:
-        op.out[sample + static_cast<std::int64_t>(t) * A + a] = e;
-        break;
-      case kUpdateDDIM: {
-        float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
-        if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
-        const float nx = op.sqrt_ap * x0 + op.sqrt_1map * e;
-        op.x[si] = nx;
-        if (op.xin != op.x) op.xin[si] = nx;
-        break;
-      }
-      case kUpdateDDPM: {
-        float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
-        if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
-        float nx = op.coef_x0 * x0 + op.coef_x * xv;
-        if (op.add_noise)
-          nx += op.sigma *
-                stream_gaussian(*op.seed, op.noise_offset + static_cast<std::uint64_t>(t) * A + a);
-        op.x[si] = nx;
-        if (op.xin != op.x) op.xin[si] = nx;
-        break;
-      }
-      case kUpdateEuler: {
-        const float nx = xv + op.dt * e;
-        op.x[si] = nx;
-        op.xin[si] = nx;
-        break;
-      }
-      case kUpdateStage: {
-        const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
-        op.kbuf[op.slot * plane + si] = e;
-        op.xin[si] = xv + op.dt * e;
-        break;
-      }
-      case kUpdateHeun: {
-        const float k1 = op.kbuf[si];
-        const float nx = xv + 0.5f * op.dt * (k1 + e);
-        op.x[si] = nx;
-        op.xin[si] = nx;
-        break;
-      }
-      case kUpdateRK4: {
-        const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
-        const float k1 = op.kbuf[si], k2 = op.kbuf[plane + si], k3 = op.kbuf[2 * plane + si];
-        const float nx = xv + (op.dt / 6.0f) * (k1 + 2.0f * k2 + 2.0f * k3 + e);
-        op.x[si] = nx;
-        op.xin[si] = nx;
-        break;
-      }
-      default:
-        break;
+    apply_update(op, sample, i / H, i % H, A, H, eps[i / H][i % H], xs[r]);  // state [A][H]
+  }
+}
+
+// Shapes outside update_kernel's instances: one wavefront per output value eps[a][t] (lanes
+// stride the c0 channels), the group statistics first (fp64, one wavefront per group).
+constexpr int kUpdGenThreads = 256;
+constexpr int kMaxUpdGenGroups = 64;
+
+__global__ __launch_bounds__(kUpdGenThreads) void update_general_kernel(UpdateOp op) {
+  __shared__ float gmean[kMaxUpdGenGroups], ginv[kMaxUpdGenGroups];
+  const int b = blockIdx.x;
+  const int A = op.action_dim, C = op.c0, H = op.horizon;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  constexpr int kWaves = kUpdGenThreads / kWave;
+  const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
+  const int cpg = C / op.groups;
+  const int n = cpg * H;
+  for (int g = wave; g < op.groups; g += kWaves) {
+    double s = 0.0, q = 0.0;
+    for (int i = lane; i < n; i += kWave) {
+      const double d = static_cast<double>(hb[static_cast<std::int64_t>(g) * n + i]);
+      s += d;
+      q += d * d;
+    }
+    s = wave_sum(s);
+    q = wave_sum(q);
+    if (lane == 0) {
+      const double cnt = static_cast<double>(n);
+      const double mean = s / cnt;
+      const double var = fmax(0.0, q / cnt - mean * mean);
+      gmean[g] = static_cast<float>(mean);
+      ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
+    }
+  }
+  __syncthreads();
+  const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
+  for (int o = wave; o < A * H; o += kWaves) {
+    const int a = o / H, t = o % H;
+    const float* wr = op.wo + static_cast<std::int64_t>(a) * C;
+    float p = 0.0f;
+    for (int c = lane; c < C; c += kWave) {
+      const int g = c / cpg;
+      const float v = mish_fast(
+          fmaf(hb[static_cast<std::int64_t>(c) * H + t] - gmean[g], ginv[g] * op.gamma[c], op.beta[c]));
+      p = fmaf(wr[c], v, p);
+    }
+#pragma unroll
+    for (int m = kWave / 2; m >= 1; m >>= 1) p += __shfl_xor(p, m, kWave);
+    if (lane == 0) {
+      const float xv = op.kind != kUpdateDenoise ? op.x[sample + o] : 0.0f;
+      apply_update(op, sample, a, t, A, H, p + op.bo[a], xv);
     }
   }
 }
@@ -375,6 +431,15 @@ __global__ void finish_kernel(const float* x, const float* amin, const float* am
 hipError_t time_mlp(const TimeSpec& times, int count, const float* w1, const float* b1,
                     const float* w2, const float* b2, int tdim, float* m, hipStream_t stream) {
   const size_t smem = static_cast<size_t>(5 * tdim) * sizeof(float);
+  if (tdim <= 0 || smem > kMaxTimeMlpLds) return hipErrorInvalidValue;
+  static bool raised = false;
+  if (!raised && smem > 64 * 1024) {
+    const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(time_mlp_kernel),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(kMaxTimeMlpLds));
+    if (st != hipSuccess) return st;
+    raised = true;
+  }
   hipLaunchKernelGGL(time_mlp_kernel, dim3(count), dim3(kBlock), smem, stream, times, w1, b1, w2,
                      b2, tdim, m);
   return hipGetLastError();
@@ -396,15 +461,22 @@ hipError_t begin_sample(const float* noise, float* x, float* xin, int batch, int
   return hipGetLastError();
 }
 
-bool update_supported(int c0, int groups, int horizon, int action_dim) {
-  return c0 > 0 && c0 <= kUpdThreads * kMaxUpdateChannelsPerLane && groups > 0 &&
-         groups <= kMaxUpdateGroups && c0 % groups == 0 && action_dim > 0 &&
+namespace {
+bool update_fused_ok(int c0, int groups, int horizon, int action_dim) {
+  return c0 <= kUpdThreads * kMaxUpdateChannelsPerLane && groups <= kMaxUpdateGroups &&
          action_dim <= kMaxActions &&
          (horizon == 1 || horizon == 2 || horizon == 4 || horizon == 8 || horizon == 16);
 }
+}  // namespace
 
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream) {
-  if (!update_supported(op.c0, op.groups, op.horizon, op.action_dim)) return hipErrorInvalidValue;
+  if (batch <= 0 || op.c0 <= 0 || op.groups <= 0 || op.groups > kMaxUpdGenGroups ||
+      op.c0 % op.groups != 0 || op.action_dim <= 0 || op.horizon <= 0)
+    return hipErrorInvalidValue;
+  if (!update_fused_ok(op.c0, op.groups, op.horizon, op.action_dim)) {
+    hipLaunchKernelGGL(update_general_kernel, dim3(batch), dim3(kUpdGenThreads), 0, stream, op);
+    return hipGetLastError();
+  }
   switch (op.horizon) {
     case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
     case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;

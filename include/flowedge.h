@@ -314,6 +314,11 @@ int fe_engine_conv_count(fe_engine* engine, size_t* count);
 int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name_capacity,
                         uint64_t* weight_bytes, uint64_t* sample_bytes);
 
+/* Kernels convolution `index` runs on in a sampling call of `batch` samples: 0 the fused
+ * weight-streaming kernels, 1 the matrix-core implicit GEMMs, 2 the general-shape kernels (shapes
+ * neither of the others has an instance for). */
+int fe_engine_conv_path(fe_engine* engine, size_t index, size_t batch, int* path);
+
 /* Launches convolutions indices[0..n) round-robin `iters` times at `batch` on the engine's stream,
  * on the kernels a sampling call of that batch uses, and returns the mean device time of one
  * launch in microseconds (hipEvents around the loop, after one untimed round).  Outputs land in

@@ -184,6 +184,22 @@ def test_denoise_matches_float64_torch_unet_tiny(tiny, t):
     np.testing.assert_allclose(eps, ref, atol=2e-5, rtol=0)
 
 
+@pytest.mark.parametrize("name", sorted(unet_ref.GENERAL_SPECS))
+def test_denoise_matches_float64_torch_unet_general_shapes(ckpt_dir, name):
+    # Kernel sizes 1 and 7, horizons 6 / 12 / 64, 3 and 64 groups, 70 action dims, width 1088:
+    # the oracle stays within float32 rounding of the float64 forward.
+    spec = unet_ref.GENERAL_SPECS[name]
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, f"general_{name}.safetensors"), spec)
+    o = oracle.Oracle(path)
+    assert (o.dims, o.horizon, o.kernel, o.groups) == (spec.dims, spec.horizon, spec.kernel,
+                                                       spec.groups)
+    cond, noise = ck.inputs(spec)
+    for t in (17.0, 0.0):
+        eps = o.denoise(cond[0], noise[0], t)
+        ref = unet_ref.torch_unet_eps(ck.read_safetensors(path), cond[0], noise[0], t)
+        np.testing.assert_allclose(eps, ref, atol=5e-6, rtol=0)
+
+
 def test_denoise_matches_float64_torch_unet_reference_fixture(fixture_ckpt):
     o = oracle.Oracle(fixture_ckpt)
     assert (o.dims, o.horizon, o.action_dim, o.cond_dim, o.kernel, o.groups) == ((8, 16), 4, 2, 3,

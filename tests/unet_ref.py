@@ -182,3 +182,24 @@ def ddim_const_eps(noise, eps_const, steps: int, T: int, clip: float | None, ami
             x0 = np.clip(x0, -clip, clip)
         x = math.sqrt(ap) * x0 + math.sqrt(1 - ap) * e
     return (x + 1) * 0.5 * (np.asarray(amax) - np.asarray(amin)) + np.asarray(amin)
+
+
+# Shapes the checkpoint format admits beyond the common U-Net configurations: odd kernel sizes
+# other than 3 and 5 (including 1), horizons that are not powers of two, more than 32 groups,
+# widths that are not multiples of 16, width * length above 8192, more than 64 action dims and a
+# final width above 1024.  Each keeps to the reference's validation (diffusion.cc:391-427).
+GENERAL_SPECS = {
+    "k7_h6_g3": ck.UNetSpec(dims=(24, 48), horizon=6, action_dim=3, cond_dim=5, kernel=7,
+                            groups=3, timestep_dim=8, train_timesteps=50, action_steps=4,
+                            obs_steps=2),
+    "h12_stages3": ck.UNetSpec(dims=(32, 64, 96), horizon=12, action_dim=4, cond_dim=6,
+                               kernel=5, groups=8, timestep_dim=16, action_steps=6),
+    "h64_wide": ck.UNetSpec(dims=(256, 512), horizon=64, action_dim=2, cond_dim=20, kernel=5,
+                            groups=8, timestep_dim=32, action_steps=8),
+    "g64_k3": ck.UNetSpec(dims=(128, 256), horizon=16, action_dim=5, cond_dim=8, kernel=3,
+                          groups=64, timestep_dim=16),
+    "a70": ck.UNetSpec(dims=(32, 64), horizon=8, action_dim=70, cond_dim=6, kernel=5, groups=8,
+                       timestep_dim=16, action_steps=4),
+    "k1_c1088": ck.UNetSpec(dims=(1088, 1088), horizon=4, action_dim=6, cond_dim=10, kernel=1,
+                            groups=8, timestep_dim=16, action_steps=2),
+}
