@@ -201,15 +201,18 @@ __device__ __forceinline__ void load_chunk(const Args& a, __amdgpu_buffer_rsrc_t
 }
 
 // LDS layout of the staged input: channel c = 4 cv + v, position t lives at
-//   ((v * NPB + t / P) * nv + cv) * P + t % P,   P = min(LIN, 4), NPB = LIN / P,
+//   (v * NPB + t / P) * (nv * P + kSwzPad) + cv * P + t % P,   P = min(LIN, 4), NPB = LIN / P,
 // so for fixed (v, t / P) the lanes of a row group (consecutive cv) read consecutive P-float
-// vectors.
+// vectors.  The staging writes run the other way (consecutive lanes hold consecutive positions,
+// then channels, i.e. consecutive planes v * NPB + t / P); the pad of 4 floats per plane moves
+// each plane to the next 16-byte bank group so those writes are free of bank conflicts too.
+constexpr int kSwzPad = 4;
 template <int LIN>
 struct Swz {
   static constexpr int P = LIN >= 4 ? 4 : LIN;
   static constexpr int NPB = LIN / P;
   __device__ static __forceinline__ int at(int c, int t, int nv) {
-    return (((c & 3) * NPB + t / P) * nv + (c >> 2)) * P + t % P;
+    return ((c & 3) * NPB + t / P) * (nv * P + kSwzPad) + (c >> 2) * P + t % P;
   }
 };
 
@@ -310,16 +313,22 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
       }
     }
     lds_barrier();
-    const int wave = tid / kWave, lane = tid & (kWave - 1);
-    for (int g = wave; g < in.groups; g += kThreads / kWave) {
+    // Sixteen lanes per group, all kMaxGroups groups in one pass: each lane sums every 16th
+    // partial of its group, a 16-lane row reduction (DPP) completes the group, and the row's
+    // first lane finishes the mean and 1/std.
+    static_assert(kThreads / 16 >= kMaxGroups, "one 16-lane row per group");
+    {
+      const int g = tid >> 4, sub = tid & 15;
       double sum = 0.0, sq = 0.0;
-      for (int i = lane; i < npg; i += kWave) {
-        sum += ps[g * npg + i];
-        sq += pq[g * npg + i];
+      if (g < in.groups) {
+        for (int i = sub; i < npg; i += 16) {
+          sum += ps[g * npg + i];
+          sq += pq[g * npg + i];
+        }
       }
-      sum = wave_sum(sum);
-      sq = wave_sum(sq);
-      if (lane == 0) {
+      sum = row_sum(sum);
+      sq = row_sum(sq);
+      if (sub == 0 && g < in.groups) {
         const double n = 4.0 * npg;
         const double mean = sum / n;
         const double var = fmax(0.0, sq / n - mean * mean);
@@ -547,8 +556,11 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
 }
 
 inline std::size_t stage_bytes(int ic, int lin, int vec) {
-  return vec == 4 ? static_cast<std::size_t>(ic) * lin * sizeof(float) : 0;
+  if (vec != 4) return 0;
+  const int planes = 4 * (lin >= 4 ? lin / 4 : 1);
+  return (static_cast<std::size_t>(ic) * lin + planes * kSwzPad) * sizeof(float);
 }
+constexpr std::size_t kMaxStageBytes = (kMaxStageFloats + 16 * kSwzPad) * sizeof(float);
 
 template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
 hipError_t launch(const Args& a, int batch, hipStream_t s) {
@@ -559,7 +571,7 @@ hipError_t launch(const Args& a, int batch, hipStream_t s) {
     if (!raised) {
       const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                static_cast<int>(kMaxStageFloats * sizeof(float)));
+                                                static_cast<int>(kMaxStageBytes));
       if (st != hipSuccess) return st;
       raised = true;
     }

@@ -319,16 +319,20 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
     }
   }
   __syncthreads();
-  const int wave = tid / kWave, lane = tid & (kWave - 1);
-  for (int g = wave; g < in.groups; g += kNaThreads / kWave) {
+  // Sixteen lanes per group (all 32 groups in one pass), a 16-lane row reduction (DPP), and the
+  // row's first lane finishes the mean and 1/std.
+  {
+    const int g = tid >> 4, sub = tid & 15;
     double s = 0.0, sq = 0.0;
-    for (int i = lane; i < npg; i += kWave) {
-      s += ps[g * npg + i];
-      sq += pq[g * npg + i];
+    if (g < in.groups) {
+      for (int i = sub; i < npg; i += 16) {
+        s += ps[g * npg + i];
+        sq += pq[g * npg + i];
+      }
     }
-    s = wave_sum(s);
-    sq = wave_sum(sq);
-    if (lane == 0) {
+    s = row_sum(s);
+    sq = row_sum(sq);
+    if (sub == 0 && g < in.groups) {
       const double n = 4.0 * npg;
       const double mean = s / n;
       const double var = fmax(0.0, sq / n - mean * mean);

@@ -95,13 +95,18 @@ __device__ __forceinline__ double lane_value(double v, int lane) {
   return __builtin_bit_cast(double, (static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
 }
 
-// Sum over the 64 lanes of a wavefront, returned to every lane: each 16-lane row is reduced with
-// DPP (quad_perm xor 1, xor 2, row_ror 4, row_ror 8), then the four row sums are read out.
-__device__ __forceinline__ double wave_sum(double v) {
+// Sum over each 16-lane row, returned to every lane of the row: DPP quad_perm xor 1, xor 2, then
+// row_ror 4 and row_ror 8.
+__device__ __forceinline__ double row_sum(double v) {
   v = dpp_add<0xb1>(v);
   v = dpp_add<0x4e>(v);
   v = dpp_add<0x124>(v);
-  v = dpp_add<0x128>(v);
+  return dpp_add<0x128>(v);
+}
+
+// Sum over the 64 lanes of a wavefront, returned to every lane: the four row sums, read out.
+__device__ __forceinline__ double wave_sum(double v) {
+  v = row_sum(v);
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
