@@ -389,12 +389,12 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
   lds_barrier();
 }
 
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool BF16>
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool BF16, int NC>
 __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean, float* ginv,
                                           float* red) {
   constexpr int LOUT = lout_of(MODE, LIN);
   constexpr int TAPS = K + (RES ? 1 : 0);
-  constexpr int NCH = chunk_budget(K, LIN, RES, VEC);
+  constexpr int NCH = NC;  // chunk slots per lane: the plan's chunk count, or the budget
   constexpr int V = RES ? 2 * LOUT : LOUT;
   const int tid = threadIdx.x;
   const int wg = blockIdx.x;
@@ -537,7 +537,7 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
   }
 }
 
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, int NC>
 __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
   constexpr int V = RES ? 2 * lout_of(MODE, LIN) : lout_of(MODE, LIN);
   static_assert(V <= kWave, "one reduced value per lane");
@@ -547,11 +547,11 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
   float* xs = reinterpret_cast<float*>(xs4);
   if constexpr (VEC == 4) {
     if (a.bf16)
-      conv_body<MODE, K, LIN, VEC, PRO, RES, true>(a, xs, gmean, ginv, red);
+      conv_body<MODE, K, LIN, VEC, PRO, RES, true, NC>(a, xs, gmean, ginv, red);
     else
-      conv_body<MODE, K, LIN, VEC, PRO, RES, false>(a, xs, gmean, ginv, red);
+      conv_body<MODE, K, LIN, VEC, PRO, RES, false, NC>(a, xs, gmean, ginv, red);
   } else {
-    conv_body<MODE, K, LIN, VEC, PRO, RES, false>(a, xs, gmean, ginv, red);
+    conv_body<MODE, K, LIN, VEC, PRO, RES, false, NC>(a, xs, gmean, ginv, red);
   }
 }
 
@@ -562,10 +562,10 @@ inline std::size_t stage_bytes(int ic, int lin, int vec) {
 }
 constexpr std::size_t kMaxStageBytes = (kMaxStageFloats + 16 * kSwzPad) * sizeof(float);
 
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
-hipError_t launch(const Args& a, int batch, hipStream_t s) {
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, int NC>
+hipError_t launch_nc(const Args& a, int batch, hipStream_t s) {
   const std::size_t smem = stage_bytes(a.ic, LIN, VEC);
-  auto fn = conv_kernel<MODE, K, LIN, VEC, PRO, RES>;
+  auto fn = conv_kernel<MODE, K, LIN, VEC, PRO, RES, NC>;
   if (smem > 48 * 1024) {  // opt in to more than 48 KB of dynamic LDS (up to 160 KB per CU)
     static bool raised = false;
     if (!raised) {
@@ -578,6 +578,22 @@ hipError_t launch(const Args& a, int batch, hipStream_t s) {
   }
   hipLaunchKernelGGL(fn, dim3(a.blocks, batch), dim3(kThreads), smem, s, a);
   return hipGetLastError();
+}
+
+// Chunk slots per lane: the plan's count when it is 1, 2 or 4 (the common plans), otherwise the
+// register budget.  Slots beyond the plan's count still issue their (out-of-range, traffic-free)
+// loads, since the loads are branch-free, so exact counts save memory-pipeline issue slots.
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
+hipError_t launch(const Args& a, int batch, hipStream_t s) {
+  constexpr int B = chunk_budget(K, LIN, RES, VEC);
+  if constexpr (VEC == 4) {
+    if (a.nch == 1) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 1>(a, batch, s);
+    if constexpr (B > 2)
+      if (a.nch == 2) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 2>(a, batch, s);
+    if constexpr (B > 4)
+      if (a.nch == 4) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 4>(a, batch, s);
+  }
+  return launch_nc<MODE, K, LIN, VEC, PRO, RES, B>(a, batch, s);
 }
 
 template <int MODE, int K, int LIN, int VEC>
