@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -440,11 +441,12 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
   const int wig = lg / kWave;
   const float* xsrc = a.in.src + b * a.in.src_stride;
   int parity = 0;
-  for (; tile < a.tiles; tile += a.blocks) {
+  // One row tile; `refill` (true for every tile but the workgroup's last) streams the next tile's
+  // weights into each chunk's registers once its products are accumulated.  The last tile is a
+  // separate instance, so it issues no refill loads at all.
+  auto do_tile = [&](int tile, auto refill) {
     const int row = tile * rpt + gid;
-    const int next = tile + a.blocks;
-    const bool more = next < a.tiles;
-    const int nrow = next * rpt + gid;
+    const int nrow = (tile + a.blocks) * rpt + gid;
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
@@ -504,8 +506,9 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
         }
       }
       // Refill this chunk's registers with the next tile's weights.
-      load_chunk<K, VEC, RES, BF16>(a, wr, rr, nrow, cv, more && j < a.nch && cv < nv && nrow < a.oc,
-                                    w[j]);
+      if constexpr (decltype(refill)::value)
+        load_chunk<K, VEC, RES, BF16>(a, wr, rr, nrow, cv, j < a.nch && cv < nv && nrow < a.oc,
+                                      w[j]);
     }
 
     rs_step<V, 32>(acc, lane);
@@ -518,7 +521,7 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
           a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + off - LOUT] =
               acc[0] + a.rbias[row];
       }
-      continue;
+      return;
     }
     // Several wavefronts per row: combine through LDS.  red holds two alternating buffers of
     // [row group][wavefront in group][V], so one barrier per tile suffices.
@@ -534,7 +537,9 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
       else
         a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + lg - LOUT] = sum + a.rbias[row];
     }
-  }
+  };
+  for (; tile + a.blocks < a.tiles; tile += a.blocks) do_tile(tile, std::true_type{});
+  do_tile(tile, std::false_type{});
 }
 
 template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, int NC>
