@@ -148,7 +148,7 @@ def dominant_roofline(eng, iters: int):
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
-        "kernel": "conv_kernel<kConvSame, K=5, LIN=4, VEC=4, kProFilm, RES=false> "
+        "kernel": "conv_kernel<kConvSame, K=5, LIN=4, VEC=4, kProFilm, RES=false, NC=4> "
                   + DOMINANT_SHAPE,
         "algorithmic_bytes_per_launch": nbytes,
         "us_per_launch": round(us, 3),

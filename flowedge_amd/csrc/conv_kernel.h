@@ -591,13 +591,11 @@ hipError_t launch_nc(const Args& a, int batch, hipStream_t s) {
 template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
 hipError_t launch(const Args& a, int batch, hipStream_t s) {
   constexpr int B = chunk_budget(K, LIN, RES, VEC);
-  if constexpr (VEC == 4) {
-    if (a.nch == 1) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 1>(a, batch, s);
-    if constexpr (B > 2)
-      if (a.nch == 2) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 2>(a, batch, s);
-    if constexpr (B > 4)
-      if (a.nch == 4) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 4>(a, batch, s);
-  }
+  if (a.nch == 1) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 1>(a, batch, s);
+  if constexpr (B > 2)
+    if (a.nch == 2) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 2>(a, batch, s);
+  if constexpr (B > 4)
+    if (a.nch == 4) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 4>(a, batch, s);
   return launch_nc<MODE, K, LIN, VEC, PRO, RES, B>(a, batch, s);
 }
 
