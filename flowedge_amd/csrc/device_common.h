@@ -31,10 +31,39 @@ __device__ __forceinline__ float bf16_to_f32(unsigned short bits) {
   return __uint_as_float(static_cast<unsigned>(bits) << 16);
 }
 
+// The value `v` of this lane's exchange partner for bit MASK, through VALU cross-lane moves: DPP
+// quad_perm (lane ^ 1, lane ^ 2), DPP row_ror 8 (lane ^ 8 within a 16-lane row) and the gfx950
+// permlane16 / permlane32 swaps (lane ^ 16, lane ^ 32).  For MASK 4 the partner is lane ^ 7 within
+// its 8-lane group (DPP row_half_mirror): it flips bit 2 and keeps the higher bits, which is all
+// the reductions below need.
+template <int MASK>
+__device__ __forceinline__ float partner(float v, int lane) {
+  const unsigned u = __float_as_uint(v);
+  unsigned r;
+  if constexpr (MASK == 1) {
+    r = __builtin_amdgcn_update_dpp(0u, u, 0xb1, 0xf, 0xf, false);
+  } else if constexpr (MASK == 2) {
+    r = __builtin_amdgcn_update_dpp(0u, u, 0x4e, 0xf, 0xf, false);
+  } else if constexpr (MASK == 4) {
+    r = __builtin_amdgcn_update_dpp(0u, u, 0x141, 0xf, 0xf, false);
+  } else if constexpr (MASK == 8) {
+    r = __builtin_amdgcn_update_dpp(0u, u, 0x128, 0xf, 0xf, false);
+  } else if constexpr (MASK == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    r = (lane & 16) ? p[0] : p[1];
+  } else {
+    static_assert(MASK == 32, "exchange bits 1 to 32");
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    r = (lane & 32) ? p[0] : p[1];
+  }
+  return __uint_as_float(r);
+}
+
 // Wavefront reduce-scatter.  On entry every lane holds N partial sums v[0..N); on exit lane l
 // holds max(N/64, 1) finished sums (over all 64 lanes) of the original indices
 // [rs_offset<N>(l), +max(N/64,1)).  Each halving step exchanges half of the remaining values with
-// the partner lane (l ^ mask); once one value remains, plain butterfly steps finish it.
+// the partner lane (see partner: it differs in the step's bit, shares the higher ones); once one
+// value remains, plain butterfly steps finish it.
 template <int N, int MASK>
 __device__ __forceinline__ void rs_step(float* v, int lane) {
   if constexpr (MASK > 0) {
@@ -44,11 +73,11 @@ __device__ __forceinline__ void rs_step(float* v, int lane) {
       for (int i = 0; i < N / 2; ++i) {
         const float send = upper ? v[i] : v[i + N / 2];
         const float keep = upper ? v[i + N / 2] : v[i];
-        v[i] = keep + __shfl_xor(send, MASK, kWave);
+        v[i] = keep + partner<MASK>(send, lane);
       }
       rs_step<N / 2, MASK / 2>(v, lane);
     } else {
-      v[0] += __shfl_xor(v[0], MASK, kWave);
+      v[0] += partner<MASK>(v[0], lane);
       rs_step<1, MASK / 2>(v, lane);
     }
   }
