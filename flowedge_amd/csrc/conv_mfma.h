@@ -39,7 +39,23 @@ struct MmArgs {
   // Byte sizes of the weight tensor and the batch of `src` / `plain` (buffer ranges of the BF16
   // kernels; each below 2 GiB).
   unsigned wbytes, srcbytes, plainbytes;
+  // Column order of a tile: 0 = (sample, position); 1 = output parity first (the F32 kernel's
+  // ConvTranspose tiles: the first half holds the even positions of its samples, the second
+  // half the odd ones).
+  int par;
 };
+
+// Sample and output position of tile column `col` (NT columns, lout positions per sample).
+__host__ __device__ inline void col_pos(int col, int nt, int lout, int par, int& bl, int& t) {
+  if (par) {
+    const int half = nt / 2, p = col >= half ? 1 : 0, c2 = col - p * half;
+    bl = c2 / (lout / 2);
+    t = 2 * (c2 - bl * (lout / 2)) + p;
+  } else {
+    bl = col / lout;
+    t = col - bl * lout;
+  }
+}
 
 // Input index read by output t through tap k, or -1 in the padding (t known only at run time).
 template <int MODE, int K, int LIN>

@@ -181,14 +181,18 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     }
   };
 
-  // Per-lane input row of every (column tile j, tap k): fixed for the whole K loop.
+  // Per-lane input row of every (column tile j, tap k): fixed for the whole K loop.  With
+  // ConvTranspose the columns are in parity order, so wavefront column half wc holds output
+  // positions of parity wc only, which taps of the other parity never reach.
+  constexpr int PAR = MODE == kConvTranspose ? 1 : 0;
   const int wr = wave >> 1, wc = wave & 1;
   const int kq = lane >> 4, l16 = lane & 15;
   int xrow[S::TJ][K];
 #pragma unroll
   for (int j = 0; j < S::TJ; ++j) {
     const int col = wc * S::WN + 16 * j + l16;
-    const int bl = col / S::LOUT, t = col - bl * S::LOUT;
+    int bl, t;
+    col_pos(col, NT, S::LOUT, PAR, bl, t);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int ti = src_at<MODE, K, LIN>(t, k);
@@ -213,6 +217,10 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     const float* X = Xs + buf * S::XFLOATS;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
+      // Output t takes tap k when t + 1 - k is even: parity wc takes the taps k = wc + 1 mod 2.
+      if constexpr (PAR) {
+        if (((k + wc + 1) & 1) != 0) continue;
+      }
       float4 av[S::TI], bv[S::TJ];
 #pragma unroll
       for (int i = 0; i < S::TI; ++i)
@@ -255,7 +263,8 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
 #pragma unroll
       for (int j = 0; j < S::TJ; ++j) {
         const int col = wc * S::WN + 16 * j + l16;
-        const int bl = col / S::LOUT, t = col - bl * S::LOUT;
+        int bl, t;
+        col_pos(col, NT, S::LOUT, PAR, bl, t);
         const int b = b0 + bl;
         if (b < a.batch)
           a.y[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] = acc[i][j][e] + bias;
@@ -276,7 +285,9 @@ __global__ __launch_bounds__(kMmThreads) void splitk_reduce_kernel(MmArgs a, int
   const int mt = tile / a.ntiles, nt = tile - mt * a.ntiles;
   const int r = local / nt_cols, c = local - r * nt_cols;
   const int oc = mt * 64 + r;
-  const int b = nt * (nt_cols / lout) + c / lout, t = c % lout;
+  int bl, t;
+  col_pos(c, nt_cols, lout, a.par, bl, t);
+  const int b = nt * (nt_cols / lout) + bl;
   if (oc < a.oc && b < a.batch)
     a.y[b * a.ys + static_cast<std::int64_t>(oc) * lout + t] = sum + a.bias[oc];
 }
@@ -483,6 +494,9 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   const bool ranges_fit = wb < (1ull << 31) && sb < (1ull << 31) && pb < (1ull << 31);
   const bool use_bf16 =
       (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
+  // The F32 kernel orders ConvTranspose tile columns by output parity (the split-K reduction
+  // reads the partial tiles in the same order).
+  a.par = !use_bf16 && op.mode == kConvTranspose ? 1 : 0;
   a.wbytes = static_cast<unsigned>(wb);
   a.srcbytes = static_cast<unsigned>(sb);
   a.plainbytes = static_cast<unsigned>(pb);
