@@ -224,6 +224,18 @@ def test_pusht_b1_ddim10_and_denoise(pusht):
             assert np.array_equal(batch[b], e.sample_diffusion(cb[b], nb[b], steps=10))
 
 
+def test_pusht_kernel_paths(pusht):
+    # The pusht U-Net's 29 convolutions per evaluation all have fused weight-streaming instances
+    # (one sample per grid row) and matrix-core instances; the switch is the batch threshold.
+    with flowedge_amd.Engine(pusht) as e:
+        names = [c["name"] for c in e.convolutions()]
+        assert len(names) == 29
+        assert e.conv_paths(1) == ["fused"] * 29
+        assert e.conv_paths(3) == ["fused"] * 29
+        assert e.conv_paths(4) == ["matrix"] * 29
+        assert e.conv_paths(256) == ["matrix"] * 29
+
+
 def test_bimanual_bf16(ckpt_dir):
     spec = ck.SPECS["bimanual"]
     path = ck.cached_checkpoint("bimanual", ckpt_dir)
