@@ -203,12 +203,13 @@ def extra_configs(iters: int = 10):
                "actions_per_sec": round(batch * spec.horizon / (ms * 1e-3), 1),
                "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                "tflops": round(tflops, 2), "finite": bool(torch.isfinite(do).all().item())}
-        if batch >= 4 and spec.bf16_weights:
+        # The engine's default matrix-core thresholds: 5 samples (F32 weights), 8 (BF16).
+        if batch >= 8 and spec.bf16_weights:
             # BF16 weights on the BF16 matrix cores, input split in two terms: two MFMA
             # products per useful product.
             row["mfma"] = "bf16 (2 products per multiply)"
             row["mfma_frac"] = round(2 * tflops / BF16_MFMA_PEAK_TFLOPS, 4)
-        elif batch >= 4:
+        elif batch >= 5 and not spec.bf16_weights:
             row["mfma"] = "fp32"
             row["mfma_frac"] = round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)
         rows.append(row)

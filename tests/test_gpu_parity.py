@@ -4,7 +4,7 @@ Tolerances (written per test): fp32 checkpoints must match within max |err| <= 1
 units (action scale (max - min)/2 = 1 for the synthetic range [-1, 1]); BF16-weight checkpoints
 are held to the same 1e-4 here because the oracle runs on the identical BF16-rounded values
 (the contract bound for BF16 variants is 2e-2).  Batches below the matrix-core threshold
-(FLOWEDGE_MFMA_BATCH, default 4 for F32 weights and 6 for BF16) run the batch-1 kernels and must
+(FLOWEDGE_MFMA_BATCH, default 5 for F32 weights and 8 for BF16) run the batch-1 kernels and must
 equal independent batch-1 calls bit for bit; larger batches run implicit GEMMs on the matrix
 cores (another summation order) and are held to the oracle per sample at the same 1e-4.
 """
@@ -231,8 +231,8 @@ def test_pusht_kernel_paths(pusht):
         names = [c["name"] for c in e.convolutions()]
         assert len(names) == 29
         assert e.conv_paths(1) == ["fused"] * 29
-        assert e.conv_paths(3) == ["fused"] * 29
-        assert e.conv_paths(4) == ["matrix"] * 29
+        assert e.conv_paths(4) == ["fused"] * 29
+        assert e.conv_paths(5) == ["matrix"] * 29
         assert e.conv_paths(256) == ["matrix"] * 29
 
 
@@ -265,7 +265,7 @@ def test_flow_full_size(ckpt_dir):
 
 
 # ---------------------------------------------------------------------------------------------
-# Batched path: the convolutions run as implicit GEMMs on the matrix cores (batch >= 4 / 6).
+# Batched path: the convolutions run as implicit GEMMs on the matrix cores (batch >= 5 / 8).
 # ---------------------------------------------------------------------------------------------
 def test_tiny_batched_mfma(tiny_engine, tiny_oracle):
     spec = ck.SPECS["tiny"]
