@@ -238,7 +238,7 @@ struct FeEngine {
   std::size_t final_in = 0;
   std::size_t xnorm = 0;       // batched path: normalised input of one convolution [B][8192]
   std::size_t splitk = 0;      // batched path: split-K partial tiles (kSplitKFloats)
-  std::size_t mfma_batch = 4;  // batches of at least this many samples use the matrix cores
+  std::size_t mfma_batch = 5;  // batches of at least this many samples use the matrix cores
   bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
   bool f32_split = false;      // F32 weights on the BF16 matrix cores (split weights and input)
 
@@ -1497,7 +1497,7 @@ std::uint64_t nfe_for(std::size_t steps, int kind, int mode) {
 }
 
 // Smallest batch that runs the convolutions on the matrix cores (FLOWEDGE_MFMA_BATCH; 0 = by
-// weight type: 4 samples for F32 convolutions, 6 for BF16, where streaming half the bytes keeps
+// weight type: 5 samples for F32 convolutions, 8 for BF16, where streaming half the bytes keeps
 // the batch-1 kernels ahead longer; a value above the max batch keeps every batch on the
 // weight-streaming kernels).
 std::size_t env_mfma_batch() {
