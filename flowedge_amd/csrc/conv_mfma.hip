@@ -525,9 +525,9 @@ hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_s
                     hipStream_t stream) {
   if (!in.norm || batch <= 0 || in.groups <= 0 || in.split % in.groups != 0)
     return hipErrorInvalidValue;
-  // Below 64 samples the one-workgroup-per-sample kernel leaves most CUs idle; the general form
-  // spreads each sample over one workgroup per group.
-  if (batch < 64 || in.groups > 32 || (in.split / in.groups * lin) % 4 != 0 ||
+  // Below 256 samples the one-workgroup-per-sample kernel leaves CUs idle; the general form
+  // spreads each sample over one workgroup per group (measured equal at 256).
+  if (batch < 256 || in.groups > 32 || (in.split / in.groups * lin) % 4 != 0 ||
       static_cast<std::int64_t>(in.split) * lin > kNaMaxFloats)
     return norm_act_general(in, lin, dst, dst_stride, batch, stream);
   switch (lin) {

@@ -92,7 +92,7 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
                      bool f32_split, hipStream_t stream);
 
 // The prologue of a ConvInput with `norm` on its own: dst[b][0 : split*lin) =
-// mish(GN(src)) [* scale + shift] [+ res], per sample.  Batches under 64 samples and shapes
+// mish(GN(src)) [* scale + shift] [+ res], per sample.  Batches under 256 samples and shapes
 // outside the per-sample kernel's instances (split * lin > 8192, more than 32 groups, groups of
 // lengths not a multiple of 4) run on norm_act_general.
 hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride, int batch,
