@@ -303,8 +303,9 @@ hipError_t conv_general(const ConvOp& op, const float* src, std::int64_t src_str
   a.mtiles = (op.oc + kGenMT - 1) / kGenMT;
   a.steps = static_cast<int>(steps);
   const std::int64_t cols = static_cast<std::int64_t>(batch) * op.lout;
-  return cols <= 16 ? launch_general<16>(a, workspace, workspace_floats, stream)
-                    : launch_general<64>(a, workspace, workspace_floats, stream);
+  if (cols <= 16) return launch_general<16>(a, workspace, workspace_floats, stream);
+  if (cols <= 32) return launch_general<32>(a, workspace, workspace_floats, stream);
+  return launch_general<64>(a, workspace, workspace_floats, stream);
 }
 
 hipError_t norm_act_general(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride,
