@@ -39,9 +39,9 @@ struct MmArgs {
   // Byte sizes of the weight tensor and the batch of `src` / `plain` (buffer ranges of the BF16
   // kernels; each below 2 GiB).
   unsigned wbytes, srcbytes, plainbytes;
-  // Column order of a tile: 0 = (sample, position); 1 = output parity first (the F32 kernel's
-  // ConvTranspose tiles: the first half holds the even positions of its samples, the second
-  // half the odd ones).
+  // Column order of a tile: 0 = (sample, position); 1 = output parity first (ConvTranspose
+  // tiles: the first half holds the even positions of its samples, the second half the odd
+  // ones).
   int par;
 };
 

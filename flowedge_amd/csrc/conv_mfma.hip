@@ -494,9 +494,9 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   const bool ranges_fit = wb < (1ull << 31) && sb < (1ull << 31) && pb < (1ull << 31);
   const bool use_bf16 =
       (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
-  // The F32 kernel orders ConvTranspose tile columns by output parity (the split-K reduction
-  // reads the partial tiles in the same order).
-  a.par = !use_bf16 && op.mode == kConvTranspose ? 1 : 0;
+  // The kernels order ConvTranspose tile columns by output parity (the split-K reduction reads
+  // the partial tiles in the same order).
+  a.par = op.mode == kConvTranspose ? 1 : 0;
   a.wbytes = static_cast<unsigned>(wb);
   a.srcbytes = static_cast<unsigned>(sb);
   a.plainbytes = static_cast<unsigned>(pb);

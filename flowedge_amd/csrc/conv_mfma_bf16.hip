@@ -236,14 +236,20 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     }
   };
 
-  // Per-lane input row of every (column tile j, tap k): fixed for the whole K loop.
+  // Per-lane input row of every (column tile j, tap k): fixed for the whole K loop.  With
+  // ConvTranspose the columns are in parity order (even output positions in the first half of
+  // the tile), so each wavefront's columns have one output parity, which taps of the other
+  // parity never reach.
+  constexpr int PAR = MODE == kConvTranspose ? 1 : 0;
   const int wr = wave / kWaveCols, wc = wave % kWaveCols;
+  const int par = 2 * wc / kWaveCols;  // output parity of this wavefront's columns (PAR)
   const int kq = lane >> 4, l16 = lane & 15;
   int xrow[S::TJ][K];
 #pragma unroll
   for (int j = 0; j < S::TJ; ++j) {
     const int col = wc * S::WN + 16 * j + l16;
-    const int bl = col / S::LOUT, t = col - bl * S::LOUT;
+    int bl, t;
+    col_pos(col, NT, S::LOUT, PAR, bl, t);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int ti = src_at<MODE, K, LIN>(t, k);
@@ -265,6 +271,10 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     const unsigned short* L = Xl + buf * S::XVALS;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
+      // Output t takes tap k when t + 1 - k is even.
+      if constexpr (PAR) {
+        if (((k + par + 1) & 1) != 0) continue;
+      }
       bf16x8 av[S::TI], al[WF32 ? S::TI : 1], bh[S::TJ], bl[S::TJ];
 #pragma unroll
       for (int i = 0; i < S::TI; ++i) {
@@ -326,7 +336,8 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
 #pragma unroll
       for (int j = 0; j < S::TJ; ++j) {
         const int col = wc * S::WN + 16 * j + l16;
-        const int bl2 = col / S::LOUT, t = col - bl2 * S::LOUT;
+        int bl2, t;
+        col_pos(col, NT, S::LOUT, PAR, bl2, t);
         const int b = b0 + bl2;
         if (b < a.batch)
           a.y[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] = acc[i][j][e] + bias;
