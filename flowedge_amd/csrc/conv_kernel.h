@@ -68,7 +68,7 @@ __host__ __device__ constexpr int chunk_budget(int k, int lin, bool res, int vec
 }
 
 // Weight floats per lane requested before the input prologue.
-constexpr int kEarlyFloats = 48;
+constexpr int kEarlyFloats = 64;
 __host__ __device__ constexpr int early_chunks(int taps) {
   return kEarlyFloats / (taps * 4) > 0 ? kEarlyFloats / (taps * 4) : 1;
 }
