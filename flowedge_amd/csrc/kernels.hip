@@ -107,8 +107,22 @@ __global__ __launch_bounds__(kBlock) void film_gemm_kernel(const float* in, std:
     }
     __syncthreads();
     if (f < fdim) {
-      for (int k = wave; k < kc; k += kBlock / kWave) {
-        const float w = wt[static_cast<std::int64_t>(k0 + k) * fdim + f];
+      // Eight weight loads in flight per lane ahead of their products (the same k order as the
+      // one-at-a-time tail, so the sums are unchanged).
+      constexpr int kStep = kBlock / kWave;
+      const float* wp = wt + static_cast<std::int64_t>(k0) * fdim + f;
+      int k = wave;
+      for (; k + 7 * kStep < kc; k += 8 * kStep) {
+        float w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = wp[static_cast<std::int64_t>(k + j * kStep) * fdim];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < kFilmRows; ++r) acc[r] = fmaf(w[j], act[r][k + j * kStep], acc[r]);
+      }
+      for (; k < kc; k += kStep) {
+        const float w = wp[static_cast<std::int64_t>(k) * fdim];
 #pragma unroll
         for (int r = 0; r < kFilmRows; ++r) acc[r] = fmaf(w, act[r][k], acc[r]);
       }
