@@ -37,7 +37,7 @@ EXPORTS = [
     "fe_engine_flow_begin_request", "fe_engine_cancel_before", "fe_engine_flow_advance",
     "fe_engine_flow_action_metadata", "fe_engine_diffusion_begin",
     "fe_engine_diffusion_begin_generation", "fe_engine_diffusion_advance",
-    "fe_weights_model_digest", "fe_engine_conv_path",
+    "fe_weights_model_digest", "fe_engine_conv_path", "fe_engine_graph_captures",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -125,6 +125,8 @@ def lib():
     L.fe_engine_sample_device.argtypes = [vp, cint, vp, vp, sz, sz, cint, u64, vp]
     L.fe_engine_prepare.argtypes = [vp, cint, sz, sz, cint]
     L.fe_device_alloc_count.restype = u64
+    L.fe_engine_graph_captures.restype = u64
+    L.fe_engine_graph_captures.argtypes = [vp]
     L.fe_engine_last_device_ms.restype = ctypes.c_float
     L.fe_engine_last_device_ms.argtypes = [vp]
     L.fe_engine_conv_count.argtypes = [vp, ctypes.POINTER(sz)]
@@ -266,6 +268,10 @@ class Engine:
         return int(lib().fe_engine_device_bytes(self._h))
 
     @property
+    def graph_captures(self) -> int:
+        return int(lib().fe_engine_graph_captures(self._h))
+
+    @property
     def last_device_ms(self) -> float:
         return float(lib().fe_engine_last_device_ms(self._h))
 
@@ -307,6 +313,7 @@ class Engine:
                          method: str = "euler") -> None:
         c = _arr(condition, (self.condition_dim,))
         n = _arr(noise, (self._values(),))
+        self._output(output)
         if method not in SOLVERS:
             raise RuntimeError("method must be 'euler', 'heun' or 'rk4'")
         self._check(lib().fe_engine_sample_condition(self._h, _p(c), _p(n), steps,
@@ -380,10 +387,16 @@ class Engine:
         return int(rem.value)
 
     # ---- batched extensions ----
-    def sample_diffusion_batch(self, condition, noise, steps: int = 10, scheduler: str = "ddim",
-                               seed: int = 0) -> np.ndarray:
+    def _batch(self, condition) -> tuple[np.ndarray, int]:
         c = _arr(condition)
         b = c.size // self.condition_dim
+        if b < 1 or c.size != b * self.condition_dim:
+            raise RuntimeError(f"condition must hold whole rows of {self.condition_dim} values")
+        return c, b
+
+    def sample_diffusion_batch(self, condition, noise, steps: int = 10, scheduler: str = "ddim",
+                               seed: int = 0) -> np.ndarray:
+        c, b = self._batch(condition)
         n = _arr(noise, (b * self._values(),))
         out = np.empty((b, self.action_horizon, self.action_dim), np.float32)
         self._check(lib().fe_engine_sample_diffusion_batch(self._h, _p(c), _p(n), b, steps,
@@ -392,8 +405,7 @@ class Engine:
 
     def sample_condition_batch(self, condition, noise, steps: int = 10,
                                method: str = "euler") -> np.ndarray:
-        c = _arr(condition)
-        b = c.size // self.condition_dim
+        c, b = self._batch(condition)
         n = _arr(noise, (b * self._values(),))
         out = np.empty((b, self.action_horizon, self.action_dim), np.float32)
         self._check(lib().fe_engine_sample_condition_batch(self._h, _p(c), _p(n), b, steps,
@@ -401,8 +413,7 @@ class Engine:
         return out
 
     def diffusion_denoise_batch(self, condition, sample, timestep: float) -> np.ndarray:
-        c = _arr(condition)
-        b = c.size // self.condition_dim
+        c, b = self._batch(condition)
         s = _arr(sample, (b * self._values(),))
         out = np.empty((b, self.action_horizon, self.action_dim), np.float32)
         self._check(lib().fe_engine_diffusion_denoise_batch(self._h, _p(c), _p(s), b,

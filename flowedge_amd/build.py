@@ -1,7 +1,8 @@
 """Build recipe for the gfx950 library (``libflowedge_amd.so``), in-tree.
 
-One hipcc invocation compiles the host runtime (C ABI, loader, graph cache) and the device
-kernels for ``--offload-arch=gfx950``.  Packed-FP32 instructions are disabled for all device code.
+Each translation unit (host runtime, loader, device kernels) is compiled by its own hipcc process
+for ``--offload-arch=gfx950`` into ``flowedge_amd/_build/``, in parallel, and the objects are
+linked into one shared library.  Packed-FP32 instructions are disabled for all device code.
 """
 
 from __future__ import annotations
@@ -9,35 +10,59 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libflowedge_amd.so")
+OBJDIR = os.path.join(HERE, "_build")
 SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/conv_fused.hip",
            "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip",
            "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/conv_general.hip",
            "csrc/identity.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-I", os.path.join(ROOT, "include")]
 
 
-def command(out: str = LIB) -> list[str]:
-    return [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
-            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-I", os.path.join(ROOT, "include"),
-            *[os.path.join(HERE, s) for s in SOURCES], "-o", out]
+def _obj(src: str) -> str:
+    return os.path.join(OBJDIR, os.path.basename(src) + ".o")
 
 
-def build(verbose: bool = False) -> str:
+def compile_command(src: str, obj: str) -> list[str]:
+    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    return [HIPCC, *FLAGS, "-c", *lang, os.path.join(HERE, src), "-o", obj]
+
+
+def link_command(out: str) -> list[str]:
+    return [HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "--hip-link",
+            *[_obj(s) for s in SOURCES], "-o", out]
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    os.makedirs(OBJDIR, exist_ok=True)
+    jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 1)))
+
+    def run(cmd):
+        return subprocess.run(cmd, capture_output=True, text=True)
+
+    with ThreadPoolExecutor(jobs) as pool:
+        results = list(pool.map(lambda s: (s, run(compile_command(s, _obj(s)))), SOURCES))
+    failed = [(s, r) for s, r in results if r.returncode != 0]
+    for s, r in results:
+        if verbose or r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+    if failed:
+        raise RuntimeError("hipcc failed on " + ", ".join(s for s, _ in failed))
     tmp = LIB + f".tmp{os.getpid()}"
-    res = subprocess.run(command(tmp), capture_output=True, text=True)
+    res = run(link_command(tmp))
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libflowedge_amd.so")
-    if verbose:
-        sys.stderr.write(res.stderr)
+        raise RuntimeError("linking libflowedge_amd.so failed")
     os.replace(tmp, LIB)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose="-v" in sys.argv))

@@ -10,7 +10,8 @@ clip_sample_range, normalization=0]``
 
 ``prediction_type`` 0 is epsilon (the reference); 1 marks the U-Net as a flow-matching velocity
 field (an extension of this library).  Conv and linear weights may be stored as BF16 (conv BF16 is
-an extension; the reference accepts BF16 only for linears).
+an extension; the reference accepts BF16 only for linears, which is the layout its converter
+writes with ``--dtype bf16``: 2-D weights BF16, everything else F32, ``convert.py:602-610``).
 
 Synthetic weights use PyTorch's default ``Conv1d``/``Linear`` initialisation bound
 ``U(-1/sqrt(fan_in), +1/sqrt(fan_in))`` for weight and bias (ConvTranspose takes ``fan_in`` from
@@ -50,7 +51,8 @@ class UNetSpec:
     clip_sample: bool = True
     clip_range: float = 1.0
     prediction: int = 0  # 0 epsilon (DDIM/DDPM), 1 velocity (flow ODE)
-    bf16_weights: bool = False
+    bf16_weights: bool = False  # every weight tensor BF16 (BF16 convolutions: an extension)
+    bf16_linears: bool = False  # only 2-D linear weights BF16 (the converter's --dtype bf16)
     action_min: tuple | None = None
     action_max: tuple | None = None
 
@@ -92,14 +94,37 @@ def splitmix_u64(seed: int, start: int, count: int) -> np.ndarray:
 
 
 def splitmix_uniform(seed: int, start: int, count: int) -> np.ndarray:
-    """Uniforms ``((z >> 40) + 1) / 16777217`` in float32 (``diffusion.cc:223-226``)."""
+    """Uniforms ``((z >> 40) + 1) / 16777217`` in float32 (``diffusion.cc:223-226``).
+
+    Computed in chunks of 2^16 calls with reused buffers (large temporaries would each be mapped
+    and faulted in afresh)."""
     out = np.empty(count, dtype=np.float32)
-    chunk = 1 << 22
-    for lo in range(0, count, chunk):
-        n = min(chunk, count - lo)
-        z = splitmix_u64(seed, start + lo, n)
-        out[lo:lo + n] = ((z >> np.uint64(40)) + np.uint64(1)).astype(np.float32) / np.float32(
-            16777217.0)
+    chunk = 1 << 16
+    base = np.arange(2, 2 + chunk, dtype=np.uint64)
+    z = np.empty(chunk, dtype=np.uint64)
+    t = np.empty(chunk, dtype=np.uint64)
+    seed64 = np.uint64(seed % (1 << 64))
+    with np.errstate(over="ignore"):
+        for lo in range(0, count, chunk):
+            n = min(chunk, count - lo)
+            zz, tt = z[:n], t[:n]
+            # state after call (start + lo + i): seed + (start + lo + i + 2) * GAMMA
+            np.add(base[:n], np.uint64(start + lo), out=zz)
+            np.multiply(zz, np.uint64(GAMMA), out=zz)
+            np.add(zz, seed64, out=zz)
+            np.right_shift(zz, np.uint64(30), out=tt)
+            np.bitwise_xor(zz, tt, out=zz)
+            np.multiply(zz, np.uint64(_M1), out=zz)
+            np.right_shift(zz, np.uint64(27), out=tt)
+            np.bitwise_xor(zz, tt, out=zz)
+            np.multiply(zz, np.uint64(_M2), out=zz)
+            np.right_shift(zz, np.uint64(31), out=tt)
+            np.bitwise_xor(zz, tt, out=zz)
+            np.right_shift(zz, np.uint64(40), out=zz)
+            np.add(zz, np.uint64(1), out=zz)
+            o = out[lo:lo + n]
+            o[...] = zz
+            np.divide(o, np.float32(16777217.0), out=o)
     return out
 
 
@@ -189,11 +214,14 @@ def synthetic_tensors(spec: UNetSpec, seed: int = 0):
         count = int(np.prod(shape))
         if kind in ("w", "b"):
             bound = np.float32(1.0 / np.sqrt(fan_in))
-            u = splitmix_uniform(seed, cursor, count)
+            values = splitmix_uniform(seed, cursor, count)
             cursor += count
-            values = ((np.float32(2.0) * u - np.float32(1.0)) * bound).astype(np.float32)
+            # (2u - 1) * bound, in place (each step rounds to float32 as the plain expression)
+            np.multiply(values, np.float32(2.0), out=values)
+            np.subtract(values, np.float32(1.0), out=values)
+            np.multiply(values, bound, out=values)
             values = values.reshape(shape)
-            if kind == "w" and spec.bf16_weights:
+            if kind == "w" and (spec.bf16_weights or (spec.bf16_linears and len(shape) == 2)):
                 values = bf16_round(values)
             yield name, values
         elif kind == "one":

@@ -175,8 +175,30 @@ struct Block {
   std::size_t film_off = 0;  // row offset of this block's 2*oc FiLM outputs
   const fe::TensorInfo* film_w = nullptr;
   const fe::TensorInfo* film_b = nullptr;
-  std::size_t h1_off = 0, h2_off = 0, r_off = 0;  // raw conv outputs [B][oc][len]
-  std::size_t xmat_off = 0;                       // materialised block input [B][ic][len]
+  int id = 0;  // index of the block's activation buffers in Work
+};
+
+// Residual blocks of a U-Net: 2 per down stage, 2 mid, 2 per up stage.
+constexpr std::size_t kMaxBlocks = 4 * kMaxStages + 2;
+
+// Per-call device buffers (the reference's WorkspacePlan, diffusion.cc:90-126,283-381): byte
+// offsets from a workspace base, planned for a batch size and a number of FiLM time rows.  The
+// engine's arena holds one Work for its max batch.
+struct Work {
+  std::size_t size = 0;
+  std::size_t batch = 0, film_rows = 0, splitk_floats = 0;
+  std::size_t time_m = 0, film_table = 0, film_cond = 0;  // [rows][tdim], [rows][F], [B][F]
+  std::size_t x_state = 0, x_in = 0, k_stages = 0;        // [B][A][H], [B][A][H], [4][B][A][H]
+  std::size_t in_cond = 0, in_noise = 0, out_action = 0;  // caller I/O staged on the device
+  std::size_t seed = 0;                                    // DDPM seed (8 bytes)
+  std::size_t concat[kMaxStages] = {};  // up stage u input [x ; skip] buffer [B][2*high][len]
+  std::size_t ds_out[kMaxStages] = {};  // downsample outputs [B][C][len/2]
+  std::size_t h1[kMaxBlocks] = {}, h2[kMaxBlocks] = {};  // raw conv outputs [B][oc][len]
+  std::size_t r[kMaxBlocks] = {};     // residual projection [B][oc][len] (non-identity blocks)
+  std::size_t xmat[kMaxBlocks] = {};  // materialised block input [B][ic][len] (identity blocks)
+  std::size_t final_in = 0, fconv_out = 0;  // [B][dims0][H]
+  std::size_t xnorm = 0;   // batched path: normalised input of one convolution
+  std::size_t splitk = 0;  // batched path: split-K partial tiles
 };
 
 struct GraphEntry {
@@ -202,9 +224,11 @@ struct FeEngine {
   std::size_t values = 0;  // H * A
   bool bf16_convs = false, any_bf16 = false;
 
-  // Arena.
+  // Arena: the weights region (load-time constants) followed by the workspace `w` for max_batch.
   char* arena = nullptr;
   std::size_t arena_bytes = 0;
+  char* ws = nullptr;  // workspace base of `w`
+  Work w;
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = -1.0f;
@@ -222,27 +246,20 @@ struct FeEngine {
   std::size_t amin = 0, amax = 0;
   Block down[kMaxStages][2];
   ConvSlot ds[kMaxStages];
-  std::size_t ds_out[kMaxStages] = {};
   Block mid[2];
   Block up[kMaxStages][2];
   ConvSlot us[kMaxStages];
-  std::size_t concat[kMaxStages] = {};  // up stage u input [x ; skip] buffer [B][2*high][len]
-  std::size_t fconv_out = 0;
   ConvSlot fconv, fout;
   NormSlot fnorm;
+  int blocks = 0;  // residual blocks (Work buffer ids 0 .. blocks-1)
   std::size_t max_nfe = 0;
-  std::size_t time_m = 0, film_table = 0, film_cond = 0;
   std::size_t ddim_table = 0;  // FiLM time rows for every train timestep [T][F] (epsilon models)
-  std::size_t x_state = 0, x_in = 0, k_stages = 0;
-  std::size_t in_cond = 0, in_noise = 0, out_action = 0, seed_dev = 0;
-  std::size_t final_in = 0;
-  std::size_t xnorm = 0;       // batched path: normalised input of one convolution [B][8192]
-  std::size_t splitk = 0;      // batched path: split-K partial tiles (kSplitKFloats)
   std::size_t mfma_batch = 5;  // batches of at least this many samples use the matrix cores
   bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
   bool f32_split = false;      // F32 weights on the BF16 matrix cores (split weights and input)
 
   std::list<GraphEntry> graphs;  // most recently used first
+  std::uint64_t captures = 0;    // graphs captured and instantiated so far
 
   // Model identity (engine_runtime.cc:159-161).
   std::array<std::uint8_t, 16> digest{};
@@ -278,11 +295,17 @@ struct FeEngine {
     std::uint64_t sample_bytes = 0;  // activations and per-channel parameters, per sample
   };
   std::vector<ConvRecord> conv_records;
-  bool recording = false;
+  bool recording = false;  // conv() keeps the arguments of every convolution it enqueues
+  bool dry = false;        // and enqueues nothing (the U-Net walk only lists its convolutions)
 
   template <typename T = float>
   T* ptr(std::size_t off) const {
     return reinterpret_cast<T*>(arena + off);
+  }
+  // A workspace buffer of the current Work.
+  template <typename T = float>
+  T* wp(std::size_t off) const {
+    return reinterpret_cast<T*>(ws + off);
   }
 
   ~FeEngine() {
@@ -381,6 +404,7 @@ struct Builder {
     if (!blk.identity && !conv(p + ".res", oc, ic, 1, fe::hip::kConvSame, blk.res)) return false;
     blk.film_off = e.film_total;
     e.film_total += 2 * oc;
+    blk.id = e.blocks++;
     for (ConvSlot* s : {&blk.c1, &blk.c2, &blk.res}) {
       s->op.lin = static_cast<int>(len);
       s->op.lout = static_cast<int>(len);
@@ -390,7 +414,6 @@ struct Builder {
 
   bool build() {
     Config& c = e.cfg;
-    const std::size_t B = e.max_batch;
     const fe::TensorInfo *w, *b;
     if (!linear_shape("dp.te1", 4 * c.tdim, c.tdim, w, b)) return false;
     e.te1w = plan.take(w->elements() * 4);
@@ -456,51 +479,61 @@ struct Builder {
     e.film_wc = plan.take(c.cond_dim * F * 4);
     e.film_bias = plan.take(F * 4);
     if (c.prediction == 0) e.ddim_table = plan.take(c.train_timesteps * F * 4);
-
-    // Per-call buffers.  U-Net evaluations per call: diffusion <= T steps, flow RK4 4 per step.
+    // U-Net evaluations per call: diffusion <= T steps, flow RK4 4 per step.
     e.max_nfe = std::max<std::size_t>(c.train_timesteps, 1024);
-    e.time_m = plan.take(e.max_nfe * c.tdim * 4);
-    e.film_table = plan.take(e.max_nfe * F * 4);
-    e.film_cond = plan.take(B * F * 4);
-    const std::size_t v = c.horizon * c.action_dim;
-    e.x_state = plan.take(B * v * 4);
-    e.x_in = plan.take(B * v * 4);
-    e.k_stages = plan.take(4 * B * v * 4);
-    e.in_cond = plan.take(B * c.cond_dim * 4);
-    e.in_noise = plan.take(B * v * 4);
-    e.out_action = plan.take(B * v * 4);
-    e.seed_dev = plan.take(8);
-
-    // Activations.  Raw conv outputs per block; the block input is materialised (by the next
-    // op's prologue) only when it is needed again as an identity residual.
-    for (std::size_t u = 0; u + 1 < c.stages; ++u) {
-      const Block& r0 = e.up[u][0];
-      e.concat[u] = plan.take(B * r0.ic * r0.len * 4);
-    }
-    auto acts = [&](Block& blk) {
-      blk.h1_off = plan.take(B * blk.oc * blk.len * 4);
-      blk.h2_off = plan.take(B * blk.oc * blk.len * 4);
-      if (!blk.identity) blk.r_off = plan.take(B * blk.oc * blk.len * 4);
-      else blk.xmat_off = plan.take(B * blk.ic * blk.len * 4);
-    };
-    for (std::size_t s = 0; s < c.stages; ++s) {
-      for (int k = 0; k < 2; ++k) acts(e.down[s][k]);
-      if (s + 1 < c.stages) e.ds_out[s] = plan.take(B * c.dims[s] * (e.down[s][1].len / 2) * 4);
-    }
-    for (int m = 0; m < 2; ++m) acts(e.mid[m]);
-    for (std::size_t u = 0; u + 1 < c.stages; ++u)
-      for (int k = 0; k < 2; ++k) acts(e.up[u][k]);
-    e.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
-    e.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
-    // Largest normalised activation (width * length of any block output).
-    std::size_t norm_floats = 0;
-    for (std::size_t st = 0; st < c.stages; ++st)
-      norm_floats = std::max(norm_floats, c.dims[st] * (c.horizon >> st));
-    e.xnorm = plan.take(B * norm_floats * 4);
-    e.splitk = plan.take(kSplitKFloats * 4);
     return true;
   }
 };
+
+// Workspace of `batch` samples with `rows` FiLM time rows and up to `splitk_floats` of split-K
+// partials.  Raw conv outputs per block; a block input is materialised (by the next op's prologue)
+// only when it is needed again as an identity residual.
+Work plan_work(const FeEngine& e, std::size_t batch, std::size_t rows, std::size_t splitk_floats) {
+  const Config& c = e.cfg;
+  const std::size_t B = batch, F = e.film_total, v = c.horizon * c.action_dim;
+  Plan plan;
+  Work w;
+  w.batch = batch;
+  w.film_rows = rows;
+  w.splitk_floats = splitk_floats;
+  w.time_m = plan.take(rows * c.tdim * 4);
+  w.film_table = plan.take(rows * F * 4);
+  w.film_cond = plan.take(B * F * 4);
+  w.x_state = plan.take(B * v * 4);
+  w.x_in = plan.take(B * v * 4);
+  w.k_stages = plan.take(4 * B * v * 4);
+  w.in_cond = plan.take(B * c.cond_dim * 4);
+  w.in_noise = plan.take(B * v * 4);
+  w.out_action = plan.take(B * v * 4);
+  w.seed = plan.take(8);
+  for (std::size_t u = 0; u + 1 < c.stages; ++u) {
+    const Block& r0 = e.up[u][0];
+    w.concat[u] = plan.take(B * r0.ic * r0.len * 4);
+  }
+  auto acts = [&](const Block& blk) {
+    w.h1[blk.id] = plan.take(B * blk.oc * blk.len * 4);
+    w.h2[blk.id] = plan.take(B * blk.oc * blk.len * 4);
+    if (!blk.identity) w.r[blk.id] = plan.take(B * blk.oc * blk.len * 4);
+    else w.xmat[blk.id] = plan.take(B * blk.ic * blk.len * 4);
+  };
+  for (std::size_t s = 0; s < c.stages; ++s) {
+    for (int k = 0; k < 2; ++k) acts(e.down[s][k]);
+    if (s + 1 < c.stages) w.ds_out[s] = plan.take(B * c.dims[s] * (e.down[s][1].len / 2) * 4);
+  }
+  for (int m = 0; m < 2; ++m) acts(e.mid[m]);
+  for (std::size_t u = 0; u + 1 < c.stages; ++u)
+    for (int k = 0; k < 2; ++k) acts(e.up[u][k]);
+  w.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
+  w.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
+  // Largest normalised activation (width * length of any block output).
+  std::size_t norm_floats = 0;
+  for (std::size_t st = 0; st < c.stages; ++st)
+    norm_floats = std::max(norm_floats, c.dims[st] * (c.horizon >> st));
+  w.xnorm = plan.take(B * norm_floats * 4);
+  w.splitk = plan.take(splitk_floats * 4);
+  w.size = plan.size;
+  return w;
+}
 
 // ---------------------------------------------------------------------------------------------
 // Uploads with repacking.
@@ -702,6 +735,7 @@ hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
     r.sample_bytes = sb;
     e.conv_records.push_back(std::move(r));
   }
+  if (e.dry) return hipSuccess;
   return dispatch_conv(e, op, res, in, y, yr, batch, s);
 }
 
@@ -731,19 +765,19 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     const float* src = in.src;
     std::int64_t ss = in.src_stride;
     if (in.norm) {
-      float* dst = in.mat != nullptr ? in.mat : e.ptr(e.xnorm);
+      float* dst = in.mat != nullptr ? in.mat : e.wp(e.w.xnorm);
       const std::int64_t ds =
           in.mat != nullptr ? in.mat_stride : static_cast<std::int64_t>(in.split) * op.lin;
       FE_TRY(norm_act(in, op.lin, dst, ds, batch, s));
       src = dst;
       ss = ds;
     }
-    float* ws = e.ptr(e.splitk);
-    FE_TRY(conv_general(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws,
-                        kSplitKFloats, s));
+    float* ws = e.wp(e.w.splitk);
+    const std::size_t wsf = e.w.splitk_floats;
+    FE_TRY(conv_general(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws, wsf, s));
     if (res != nullptr)
-      FE_TRY(conv_general(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws,
-                          kSplitKFloats, s));
+      FE_TRY(conv_general(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws, wsf,
+                          s));
     return hipSuccess;
   }
   if (path == ConvPath::kMatrix) {
@@ -751,19 +785,20 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     const float* src = in.src;
     std::int64_t ss = in.src_stride;
     if (in.norm) {
-      float* dst = in.mat != nullptr ? in.mat : e.ptr(e.xnorm);
+      float* dst = in.mat != nullptr ? in.mat : e.wp(e.w.xnorm);
       const std::int64_t ds =
           in.mat != nullptr ? in.mat_stride : static_cast<std::int64_t>(in.split) * op.lin;
       FE_TRY(norm_act(in, op.lin, dst, ds, batch, s));
       src = dst;
       ss = ds;
     }
-    float* ws = e.ptr(e.splitk);
-    FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws,
-                     kSplitKFloats, e.bf16_mma, e.f32_split, s));
+    float* ws = e.wp(e.w.splitk);
+    const std::size_t wsf = e.w.splitk_floats;
+    FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws, wsf,
+                     e.bf16_mma, e.f32_split, s));
     if (res != nullptr)
-      FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws,
-                       kSplitKFloats, e.bf16_mma, e.f32_split, s));
+      FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws, wsf,
+                       e.bf16_mma, e.f32_split, s));
     return hipSuccess;
   }
   return conv_fused(op, res, in, y, yr, batch, s);
@@ -810,8 +845,8 @@ hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, c
   using namespace fe::hip;
   hipStream_t s = e.stream;
   const std::int64_t act = static_cast<std::int64_t>(b.oc * b.len);
-  float* h1 = e.ptr(b.h1_off);
-  float* h2 = e.ptr(b.h2_off);
+  float* h1 = e.wp(e.w.h1[b.id]);
+  float* h2 = e.wp(e.w.h2[b.id]);
   // Where the (virtual) input is materialised, when something reads it again.
   float* mat = nullptr;
   std::int64_t mat_stride = 0;
@@ -820,12 +855,12 @@ hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, c
       mat = skip_mat;
       mat_stride = skip_stride;
     } else if (b.identity) {
-      mat = e.ptr(b.xmat_off);
+      mat = e.wp(e.w.xmat[b.id]);
       mat_stride = static_cast<std::int64_t>(b.ic * b.len);
     }
   }
   ConvInput ci = input_of(e, in, mat, mat_stride);
-  float* r = b.identity ? nullptr : e.ptr(b.r_off);
+  float* r = b.identity ? nullptr : e.wp(e.w.r[b.id]);
   FE_TRY(conv(e, site + ".conv1", b.c1.op, b.identity ? nullptr : &b.res.op, ci, View{h1, act},
               View{r, act}, batch, s));
   ConvInput c2{};
@@ -837,7 +872,7 @@ hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, c
   c2.beta = e.ptr(b.n1.b_off);
   c2.groups = static_cast<int>(e.cfg.groups);
   c2.film_time = film_row;
-  c2.film_cond = e.ptr(e.film_cond);
+  c2.film_cond = e.wp(e.w.film_cond);
   c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
   c2.film_off = static_cast<int>(b.film_off);
   FE_TRY(conv(e, site + ".conv2", b.c2.op, nullptr, c2, View{h2, act}, View{}, batch, s));
@@ -865,7 +900,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
   const Config& c = e.cfg;
   hipStream_t s = e.stream;
   Act x;
-  x.p = e.ptr(e.x_in);
+  x.p = e.wp(e.w.x_in);
   x.stride = static_cast<std::int64_t>(c.action_dim * c.horizon);
   x.channels = static_cast<int>(c.action_dim);
   Act y;
@@ -883,11 +918,11 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       std::int64_t skip_stride = 0;
       if (st >= 1) {
         const std::size_t u = c.stages - 1 - st;
-        skip = e.ptr(e.concat[u]) + d.op.ic * d.op.lin;
+        skip = e.wp(e.w.concat[u]) + d.op.ic * d.op.lin;
         skip_stride = static_cast<std::int64_t>(e.up[u][0].ic * e.up[u][0].len);
       }
       ConvInput ci = input_of(e, x, skip, skip_stride);
-      float* out = e.ptr(e.ds_out[st]);
+      float* out = e.wp(e.w.ds_out[st]);
       const std::int64_t os = static_cast<std::int64_t>(d.op.oc) * d.op.lout;
       FE_TRY(conv(e, stage + ".downsample", d.op, nullptr, ci, View{out, os}, View{}, batch, s));
       x = Act{};
@@ -900,7 +935,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
   // of up stage 0.
   {
     const Block& m0 = e.mid[0];
-    float* skip = e.ptr(e.concat[0]) + m0.ic * m0.len;
+    float* skip = e.wp(e.w.concat[0]) + m0.ic * m0.len;
     const std::int64_t skip_stride = static_cast<std::int64_t>(e.up[0][0].ic * e.up[0][0].len);
     FE_TRY(enqueue_block(e, "mid0", m0, x, batch, film_row, skip, skip_stride, y));
     x = y;
@@ -917,7 +952,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
     if (u == 0) {
       cat = x;
     } else {
-      cat.p = e.ptr(e.concat[u]);
+      cat.p = e.wp(e.w.concat[u]);
       cat.stride = cs;
       cat.channels = half;
     }
@@ -929,13 +964,13 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       hipStream_t s2 = e.stream;
       const std::int64_t act = static_cast<std::int64_t>(r0.oc * r0.len);
       ConvInput ci = input_of(e, in, nullptr, 0);
-      ci.plain = e.ptr(e.concat[u]) + half * r0.len;
+      ci.plain = e.wp(e.w.concat[u]) + half * r0.len;
       ci.plain_stride = cs;
       const std::string stage = "up" + std::to_string(u);
-      FE_TRY(conv(e, stage + ".b0.conv1", r0.c1.op, &r0.res.op, ci, View{e.ptr(r0.h1_off), act},
-                  View{e.ptr(r0.r_off), act}, batch, s2));
+      FE_TRY(conv(e, stage + ".b0.conv1", r0.c1.op, &r0.res.op, ci, View{e.wp(e.w.h1[r0.id]), act},
+                  View{e.wp(e.w.r[r0.id]), act}, batch, s2));
       ConvInput c2{};
-      c2.src = e.ptr(r0.h1_off);
+      c2.src = e.wp(e.w.h1[r0.id]);
       c2.src_stride = act;
       c2.split = static_cast<int>(r0.oc);
       c2.norm = true;
@@ -943,18 +978,18 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
       c2.beta = e.ptr(r0.n1.b_off);
       c2.groups = static_cast<int>(c.groups);
       c2.film_time = film_row;
-      c2.film_cond = e.ptr(e.film_cond);
+      c2.film_cond = e.wp(e.w.film_cond);
       c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
       c2.film_off = static_cast<int>(r0.film_off);
-      FE_TRY(conv(e, stage + ".b0.conv2", r0.c2.op, nullptr, c2, View{e.ptr(r0.h2_off), act},
+      FE_TRY(conv(e, stage + ".b0.conv2", r0.c2.op, nullptr, c2, View{e.wp(e.w.h2[r0.id]), act},
                   View{}, batch, s2));
       y = Act{};
       y.virt = true;
-      y.p = e.ptr(r0.h2_off);
+      y.p = e.wp(e.w.h2[r0.id]);
       y.stride = act;
       y.gamma = e.ptr(r0.n2.g_off);
       y.beta = e.ptr(r0.n2.b_off);
-      y.res = e.ptr(r0.r_off);
+      y.res = e.wp(e.w.r[r0.id]);
       y.res_stride = act;
       y.channels = static_cast<int>(r0.oc);
       x = y;
@@ -966,10 +1001,10 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
     const ConvSlot& up = e.us[u];
     View dst;
     if (u + 2 < c.stages) {
-      dst.p = e.ptr(e.concat[u + 1]);
+      dst.p = e.wp(e.w.concat[u + 1]);
       dst.stride = static_cast<std::int64_t>(e.up[u + 1][0].ic * e.up[u + 1][0].len);
     } else {
-      dst.p = e.ptr(e.final_in);
+      dst.p = e.wp(e.w.final_in);
       dst.stride = static_cast<std::int64_t>(c.dims[0] * c.horizon);
     }
     ConvInput ci = input_of(e, x, nullptr, 0);
@@ -977,9 +1012,9 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
                 s));
   }
   const std::int64_t fs = static_cast<std::int64_t>(c.dims[0] * c.horizon);
-  float* fo = e.ptr(e.fconv_out);
+  float* fo = e.wp(e.w.fconv_out);
   ConvInput fi{};
-  fi.src = e.ptr(e.final_in);
+  fi.src = e.wp(e.w.final_in);
   fi.src_stride = fs;
   fi.split = static_cast<int>(c.dims[0]);
   FE_TRY(conv(e, "final.conv", e.fconv.op, nullptr, fi, View{fo, fs}, View{}, batch, s));
@@ -992,6 +1027,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
   upd.groups = static_cast<int>(kFinalNormGroups);
   upd.wo = static_cast<const float*>(e.fout.op.w);
   upd.bo = e.fout.op.b;
+  if (e.dry) return hipSuccess;
   return update(upd, batch, s);
 }
 
@@ -1005,25 +1041,27 @@ hipError_t enqueue_film_time(FeEngine& e, const fe::hip::TimeSpec& ts, int count
   const Config& c = e.cfg;
   const int F = static_cast<int>(e.film_total);
   FE_TRY(time_mlp(ts, count, e.ptr(e.te1w), e.ptr(e.te1b), e.ptr(e.te2w), e.ptr(e.te2b),
-                  static_cast<int>(c.tdim), e.ptr(e.time_m), e.stream));
-  return film_gemm(e.ptr(e.time_m), static_cast<std::int64_t>(c.tdim), count,
+                  static_cast<int>(c.tdim), e.wp(e.w.time_m), e.stream));
+  return film_gemm(e.wp(e.w.time_m), static_cast<std::int64_t>(c.tdim), count,
                    static_cast<int>(c.tdim), e.ptr(e.film_wt), e.ptr(e.film_bias), F, false, table,
                    F, e.stream);
 }
 
 // Condition part W_c mish(cond_b) for every sample; once per sampling call (the condition is
-// the same for every U-Net evaluation of a call).
-hipError_t enqueue_film_cond(FeEngine& e, int batch) {
+// the same for every U-Net evaluation of a call).  `cond` defaults to the staged input buffer.
+hipError_t enqueue_film_cond(FeEngine& e, int batch, const float* cond = nullptr) {
   const Config& c = e.cfg;
   const int F = static_cast<int>(e.film_total);
-  return fe::hip::film_gemm(e.ptr(e.in_cond), static_cast<std::int64_t>(c.cond_dim), batch,
+  return fe::hip::film_gemm(cond != nullptr ? cond : e.wp(e.w.in_cond),
+                            static_cast<std::int64_t>(c.cond_dim), batch,
                             static_cast<int>(c.cond_dim), e.ptr(e.film_wc), nullptr, F, true,
-                            e.ptr(e.film_cond), F, e.stream);
+                            e.wp(e.w.film_cond), F, e.stream);
 }
 
-hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int batch) {
-  FE_TRY(enqueue_film_time(e, ts, count, e.ptr(e.film_table)));
-  return enqueue_film_cond(e, batch);
+hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int batch,
+                        const float* cond = nullptr) {
+  FE_TRY(enqueue_film_time(e, ts, count, e.wp(e.w.film_table)));
+  return enqueue_film_cond(e, batch, cond);
 }
 
 // DDIM/DDPM sampling (diffusion.cc:916-1035) for `batch` samples, in three parts so that a
@@ -1032,7 +1070,7 @@ hipError_t enqueue_film(FeEngine& e, const fe::hip::TimeSpec& ts, int count, int
 hipError_t enqueue_diffusion_start(FeEngine& e, int batch) {
   using namespace fe::hip;
   const Config& c = e.cfg;
-  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
+  FE_TRY(begin_sample(e.wp(e.w.in_noise), e.wp(e.w.x_state), e.wp(e.w.x_in), batch,
                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
   return enqueue_film_cond(e, batch);
 }
@@ -1048,8 +1086,8 @@ hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int
   const float ap = prev >= 0 ? alphas[prev] : 1.0f;
   const float bt = 1.0f - at;
   UpdateOp u{};
-  u.x = e.ptr(e.x_state);
-  u.xin = e.ptr(e.x_in);
+  u.x = e.wp(e.w.x_state);
+  u.xin = e.wp(e.w.x_in);
   u.sqrt_at = std::sqrt(at);
   u.sqrt_bt = std::sqrt(bt);
   u.clip = c.clip ? 1 : 0;
@@ -1067,7 +1105,7 @@ hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int
     u.coef_x = std::sqrt(ca) * (1.0f - ap) / std::max(bt, 1e-20f);
     const float var = ((1.0f - ap) / std::max(bt, 1e-20f)) * cb;
     u.sigma = std::sqrt(std::max(var, 1e-20f));
-    u.seed = e.ptr<std::uint64_t>(e.seed_dev);
+    u.seed = e.wp<std::uint64_t>(e.w.seed);
     u.add_noise = prev >= 0 ? 1 : 0;
     u.noise_offset = static_cast<std::uint64_t>(i) * e.values;
   }
@@ -1077,8 +1115,8 @@ hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int
 
 hipError_t enqueue_diffusion_readout(FeEngine& e, int batch) {
   const Config& c = e.cfg;
-  return fe::hip::finish_sample(e.ptr(e.x_state), e.ptr(e.amin), e.ptr(e.amax),
-                                e.ptr(e.out_action), batch, static_cast<int>(c.horizon),
+  return fe::hip::finish_sample(e.wp(e.w.x_state), e.ptr(e.amin), e.ptr(e.amax),
+                                e.wp(e.w.out_action), batch, static_cast<int>(c.horizon),
                                 static_cast<int>(c.action_dim), e.stream);
 }
 
@@ -1099,7 +1137,7 @@ std::size_t flow_stages(int method) {
 hipError_t enqueue_flow_start(FeEngine& e, int batch, std::size_t steps, int method) {
   using namespace fe::hip;
   const Config& c = e.cfg;
-  FE_TRY(begin_sample(e.ptr(e.in_noise), e.ptr(e.x_state), e.ptr(e.x_in), batch,
+  FE_TRY(begin_sample(e.wp(e.w.in_noise), e.wp(e.w.x_state), e.wp(e.w.x_in), batch,
                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
   TimeSpec ts;
   ts.mode = kTimesFlow;
@@ -1116,9 +1154,9 @@ hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int meth
   const float half_dt = 0.5f * dt;
   for (int j = 0; j < stages; ++j) {
     UpdateOp u{};
-    u.x = e.ptr(e.x_state);
-    u.xin = e.ptr(e.x_in);
-    u.kbuf = e.ptr(e.k_stages);
+    u.x = e.wp(e.w.x_state);
+    u.xin = e.wp(e.w.x_in);
+    u.kbuf = e.wp(e.w.k_stages);
     u.dt = dt;
     if (stages == 1) {
       u.kind = kUpdateEuler;
@@ -1140,7 +1178,7 @@ hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int meth
       }
     }
     const std::size_t n = step * static_cast<std::size_t>(stages) + static_cast<std::size_t>(j);
-    FE_TRY(enqueue_unet(e, batch, e.ptr(e.film_table) + n * e.film_total, u));
+    FE_TRY(enqueue_unet(e, batch, e.wp(e.w.film_table) + n * e.film_total, u));
   }
   return hipSuccess;
 }
@@ -1148,7 +1186,7 @@ hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int meth
 hipError_t enqueue_flow_readout(FeEngine& e, int batch) {
   // flow.cc:321: the flow head returns x(1) as is (no unnormalisation).
   const Config& c = e.cfg;
-  return fe::hip::finish_sample(e.ptr(e.x_state), nullptr, nullptr, e.ptr(e.out_action), batch,
+  return fe::hip::finish_sample(e.wp(e.w.x_state), nullptr, nullptr, e.wp(e.w.out_action), batch,
                                 static_cast<int>(c.horizon), static_cast<int>(c.action_dim),
                                 e.stream);
 }
@@ -1192,6 +1230,7 @@ hipError_t capture_graph(FeEngine& e, Body&& body, hipGraphExec_t& exec) {
   st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   (void)hipGraphDestroy(graph);
   if (st != hipSuccess) exec = nullptr;
+  else ++e.captures;
   return st;
 }
 
@@ -1229,32 +1268,27 @@ int hip_fail(const char* what, hipError_t st) {
   return FE_STATUS_RESOURCE_EXHAUSTED;
 }
 
-// Validates a sampling request (engine_runtime.cc:446-470 + extensions).
-// Records the convolutions of one U-Net evaluation (batch 1, eager, on whatever the buffers hold)
-// the first time a diagnostic asks for them.
+// Lists the convolutions of one U-Net evaluation (their arguments at batch 1) the first time a
+// diagnostic asks for them, by walking the U-Net without enqueueing anything.
 int ensure_conv_records(FeEngine* e) {
   if (!e->conv_records.empty()) return FE_STATUS_OK;
-  hipError_t st = hipSetDevice(e->device);
-  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
   using namespace fe::hip;
-  TimeSpec ts;
-  ts.mode = kTimesSingle;
-  ts.t0 = 0.0f;
   UpdateOp u{};
   u.kind = kUpdateDenoise;
-  u.out = e->ptr(e->out_action);
-  end_solve(e);
+  u.out = e->wp(e->w.out_action);
   e->recording = true;
-  st = enqueue_film(*e, ts, 1, 1);
-  if (st == hipSuccess) st = enqueue_unet(*e, 1, e->ptr(e->film_table), u);
+  e->dry = true;
+  const hipError_t st = enqueue_unet(*e, 1, e->wp(e->w.film_table), u);
   e->recording = false;
-  if (st == hipSuccess) st = hipStreamSynchronize(e->stream);
+  e->dry = false;
   if (st != hipSuccess) {
     e->conv_records.clear();
-    return hip_fail("Diagnostic U-Net evaluation failed", st);
+    return hip_fail("Diagnostic U-Net walk failed", st);
   }
   return FE_STATUS_OK;
 }
+
+// Validates a sampling request (engine_runtime.cc:446-470 + extensions).
 
 int check_sample(const FeEngine* e, int kind, std::size_t batch, std::size_t steps, int mode) {
   if (kind == 0) {
@@ -1317,16 +1351,16 @@ int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, st
   std::memcpy(e->pin_cond, cond, nc * 4);
   std::memcpy(e->pin_noise, noise, nv * 4);
   *e->pin_seed = seed;
-  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), e->pin_cond, nc * 4, hipMemcpyHostToDevice,
+  if ((st = hipMemcpyAsync(e->wp(e->w.in_cond), e->pin_cond, nc * 4, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->in_noise), e->pin_noise, nv * 4, hipMemcpyHostToDevice,
+      (st = hipMemcpyAsync(e->wp(e->w.in_noise), e->pin_noise, nv * 4, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->seed_dev), e->pin_seed, 8, hipMemcpyHostToDevice,
+      (st = hipMemcpyAsync(e->wp(e->w.seed), e->pin_seed, 8, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess)
     return hip_fail("Input upload failed", st);
   const int r = run_graph(e, kind, batch, steps, mode);
   if (r != FE_STATUS_OK) return r;
-  if ((st = hipMemcpyAsync(e->pin_action, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToHost,
+  if ((st = hipMemcpyAsync(e->pin_action, e->wp(e->w.out_action), nv * 4, hipMemcpyDeviceToHost,
                            e->stream)) != hipSuccess ||
       (st = hipStreamSynchronize(e->stream)) != hipSuccess)
     return hip_fail("Sampling failed", st);
@@ -1424,11 +1458,11 @@ int solve_begin(FeEngine* e, const float* cond, const float* noise, const SolveR
   std::memcpy(e->pin_cond, cond, e->cfg.cond_dim * 4);
   std::memcpy(e->pin_noise, noise, e->values * 4);
   *e->pin_seed = r.seed;
-  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), e->pin_cond, e->cfg.cond_dim * 4,
+  if ((st = hipMemcpyAsync(e->wp(e->w.in_cond), e->pin_cond, e->cfg.cond_dim * 4,
                            hipMemcpyHostToDevice, e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->in_noise), e->pin_noise, e->values * 4,
+      (st = hipMemcpyAsync(e->wp(e->w.in_noise), e->pin_noise, e->values * 4,
                            hipMemcpyHostToDevice, e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->seed_dev), e->pin_seed, 8, hipMemcpyHostToDevice,
+      (st = hipMemcpyAsync(e->wp(e->w.seed), e->pin_seed, 8, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess ||
       (st = hipGraphLaunch(v.graphs[0], e->stream)) != hipSuccess ||
       (st = hipStreamSynchronize(e->stream)) != hipSuccess)
@@ -1475,7 +1509,7 @@ int solve_advance(FeEngine* e, int kind, std::size_t budget, float* action,
     ++v.next;
   }
   const std::size_t nv = e->values;
-  if ((st = hipMemcpyAsync(e->pin_action, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToHost,
+  if ((st = hipMemcpyAsync(e->pin_action, e->wp(e->w.out_action), nv * 4, hipMemcpyDeviceToHost,
                            e->stream)) != hipSuccess ||
       (st = hipStreamSynchronize(e->stream)) != hipSuccess) {
     v.active = false;
@@ -1565,7 +1599,9 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     set_error(builder.err);
     return nullptr;
   }
-  e->arena_bytes = builder.plan.size;
+  const std::size_t work_base = (builder.plan.size + kAlign - 1) / kAlign * kAlign;
+  e->w = plan_work(*e, e->max_batch, e->max_nfe, kSplitKFloats);
+  e->arena_bytes = work_base + e->w.size;
   // Measured crossovers (DDIM-10 ticks): the fused weight-streaming kernels stay faster through
   // 4 samples with F32 weights and 7 with BF16 weights.
   if (e->mfma_batch == 0) e->mfma_batch = e->bf16_convs ? 8 : 5;
@@ -1591,6 +1627,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     return nullptr;
   }
   g_device_allocs.fetch_add(1);
+  e->ws = e->arena + work_base;
   const std::size_t B = e->max_batch, nv = B * e->values, nc = B * e->cfg.cond_dim;
   const std::size_t pin_bytes = (nc + 2 * nv) * 4 + 64;
   void* pin = nullptr;
@@ -1848,6 +1885,10 @@ int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
     set_error("Invalid arguments to fe_engine_diffusion_denoise");
     return FE_STATUS_INVALID_ARGUMENT;
   }
+  if (engine->cfg.prediction != 0) {
+    set_error("Model has no Diffusion Policy head");  // engine_runtime.cc:476-479
+    return FE_STATUS_UNSUPPORTED_MODEL;
+  }
   if (batch > engine->max_batch) {
     set_error("Batch size must be between 1 and the engine's max batch");
     return FE_STATUS_INVALID_ARGUMENT;
@@ -1861,9 +1902,9 @@ int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
   std::memcpy(e->pin_cond, condition, nc * 4);
   std::memcpy(e->pin_noise, normalized_sample, nv * 4);
   using namespace fe::hip;
-  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), e->pin_cond, nc * 4, hipMemcpyHostToDevice,
+  if ((st = hipMemcpyAsync(e->wp(e->w.in_cond), e->pin_cond, nc * 4, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->in_noise), e->pin_noise, nv * 4, hipMemcpyHostToDevice,
+      (st = hipMemcpyAsync(e->wp(e->w.in_noise), e->pin_noise, nv * 4, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess)
     return hip_fail("Input upload failed", st);
   const int b = static_cast<int>(batch);
@@ -1872,13 +1913,13 @@ int fe_engine_diffusion_denoise_batch(fe_engine* engine, const float* condition,
   ts.t0 = timestep;
   UpdateOp u{};
   u.kind = kUpdateDenoise;
-  u.out = e->ptr(e->out_action);
-  if ((st = begin_sample(e->ptr(e->in_noise), e->ptr(e->x_in), e->ptr(e->x_in), b,
+  u.out = e->wp(e->w.out_action);
+  if ((st = begin_sample(e->wp(e->w.in_noise), e->wp(e->w.x_in), e->wp(e->w.x_in), b,
                          static_cast<int>(c.horizon), static_cast<int>(c.action_dim),
                          e->stream)) != hipSuccess ||
       (st = enqueue_film(*e, ts, 1, b)) != hipSuccess ||
-      (st = enqueue_unet(*e, b, e->ptr(e->film_table), u)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->pin_action, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToHost,
+      (st = enqueue_unet(*e, b, e->wp(e->w.film_table), u)) != hipSuccess ||
+      (st = hipMemcpyAsync(e->pin_action, e->wp(e->w.out_action), nv * 4, hipMemcpyDeviceToHost,
                            e->stream)) != hipSuccess ||
       (st = hipStreamSynchronize(e->stream)) != hipSuccess)
     return hip_fail("Diffusion denoiser execution failed", st);
@@ -1910,16 +1951,16 @@ int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_
   end_solve(e);
   const std::size_t nc = batch * e->cfg.cond_dim, nv = batch * e->values;
   *e->pin_seed = seed;
-  if ((st = hipMemcpyAsync(e->ptr(e->in_cond), condition_dev, nc * 4, hipMemcpyDeviceToDevice,
+  if ((st = hipMemcpyAsync(e->wp(e->w.in_cond), condition_dev, nc * 4, hipMemcpyDeviceToDevice,
                            e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->in_noise), noise_dev, nv * 4, hipMemcpyDeviceToDevice,
+      (st = hipMemcpyAsync(e->wp(e->w.in_noise), noise_dev, nv * 4, hipMemcpyDeviceToDevice,
                            e->stream)) != hipSuccess ||
-      (st = hipMemcpyAsync(e->ptr(e->seed_dev), e->pin_seed, 8, hipMemcpyHostToDevice,
+      (st = hipMemcpyAsync(e->wp(e->w.seed), e->pin_seed, 8, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess)
     return hip_fail("Input copy failed", st);
   const int r = run_graph(e, kind, batch, steps, mode);
   if (r != FE_STATUS_OK) return r;
-  if ((st = hipMemcpyAsync(action_dev, e->ptr(e->out_action), nv * 4, hipMemcpyDeviceToDevice,
+  if ((st = hipMemcpyAsync(action_dev, e->wp(e->w.out_action), nv * 4, hipMemcpyDeviceToDevice,
                            e->stream)) != hipSuccess ||
       (st = hipStreamSynchronize(e->stream)) != hipSuccess)
     return hip_fail("Sampling failed", st);
@@ -2134,6 +2175,10 @@ size_t fe_engine_device_bytes(const fe_engine* engine) {
 }
 
 uint64_t fe_device_alloc_count(void) { return g_device_allocs.load(); }
+
+uint64_t fe_engine_graph_captures(const fe_engine* engine) {
+  return engine != nullptr ? engine->captures : 0;
+}
 
 int fe_engine_conv_count(fe_engine* engine, size_t* count) {
   clear_error();

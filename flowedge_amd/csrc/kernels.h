@@ -185,4 +185,5 @@ hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
 hipError_t finish_sample(const float* x, const float* amin, const float* amax, float* action,
                          int batch, int horizon, int action_dim, hipStream_t stream);
 
+
 }  // namespace fe::hip

@@ -287,8 +287,16 @@ int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_
                             const float* noise_dev, size_t batch, size_t steps, int mode,
                             uint64_t seed, float* action_dev);
 
-/* Build (capture and instantiate) the sampling graph for this shape ahead of the first call. */
+/* Build (capture and instantiate) the sampling graph for this shape ahead of the first call.
+ * A sampling call of a (kind, batch, steps, mode) with no cached graph captures one itself
+ * (HIP-runtime host and kernel-argument allocations, about a millisecond); the engine keeps the
+ * 32 most recently used.  After a shape's first call or prepare, its calls allocate nothing and
+ * capture nothing while it stays cached. */
 int fe_engine_prepare(fe_engine* engine, int kind, size_t batch, size_t steps, int mode);
+
+/* Sampling graphs this engine has captured and instantiated so far (sampling, prepare and
+ * resumable-solve graphs). */
+uint64_t fe_engine_graph_captures(const fe_engine* engine);
 
 /* Largest batch the arena was sized for (FLOWEDGE_MAX_BATCH at load, default 256). */
 size_t fe_engine_max_batch(const fe_engine* engine);
@@ -305,8 +313,8 @@ uint64_t fe_device_alloc_count(void);
 float fe_engine_last_device_ms(const fe_engine* engine);
 
 /* Diagnostics (no counterpart in the reference; for benchmarks and profiling).  The fused
- * convolutions of one U-Net evaluation, in launch order, recorded from an eager batch-1
- * evaluation on the engine's current buffers the first time they are asked for. */
+ * convolutions of one U-Net evaluation, in launch order, with their batch-1 arguments, listed
+ * the first time they are asked for (nothing runs on the device to list them). */
 int fe_engine_conv_count(fe_engine* engine, size_t* count);
 
 /* Name ("site [oc<-ic Kk Llin prologue]") and algorithmic bytes of convolution `index`: weights

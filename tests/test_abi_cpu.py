@@ -183,6 +183,68 @@ def test_fingerprint_covers_every_hash_branch_and_skips_other_dtypes(tmp_path):
     assert flowedge_amd.weights_digest(without) == flowedge_amd.weights_digest(p)
 
 
+def test_header_reader_honours_json_strings(tmp_path):
+    # Tensor names and other strings holding braces, quotes, backslashes, a dtype's text or
+    # escaped unicode are decoded as JSON: every F32/BF16 tensor is found under its exact name
+    # (the digest hashes each name) and an I8 entry carrying the text "F32" is still skipped.
+    import json
+    import struct
+
+    import numpy as np
+
+    from oracle import fingerprint
+    raw = np.arange(8, dtype=np.float32).tobytes()
+    entries = [
+        ("a{b}c", {"dtype": "F32", "shape": [2, 4]}),
+        ('quote"d', {"dtype": "F32", "shape": [8]}),
+        ("back\\slash", {"dtype": "BF16", "shape": [4, 4]}),
+        ('"F32"', {"dtype": "F32", "shape": [1, 8], "note": "} { \" ]"}),
+        ("caf\u00e9", {"dtype": "F32", "shape": [8]}),
+        ("skip", {"dtype": "I8", "shape": [32], "comment": "\"F32\""}),
+    ]
+    header = {"__metadata__": {"format": "pt", "odd": "a } b { c \" d"}}
+    off = 0
+    for name, ent in entries:
+        header[name] = dict(ent, data_offsets=[off, off + len(raw)])
+        off += len(raw)
+    js = json.dumps(header).encode()  # ensure_ascii: the unicode name is written as \u00e9
+    assert b"\\u00e9" in js
+    js += b" " * ((8 - len(js) % 8) % 8)
+    path = tmp_path / "names.safetensors"
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(js)) + js + raw * len(entries))
+    lib = flowedge_amd.lib()
+    w = lib.fe_weights_load(str(path).encode())
+    assert w, flowedge_amd.last_error()
+    try:
+        assert lib.fe_weights_size_bytes(w) == 5 * len(raw)
+    finally:
+        lib.fe_weights_free(w)
+    names = [t[0] for t in fingerprint.tensors_in_order(str(path))]
+    assert names == ["a{b}c", 'quote"d', "back\\slash", '"F32"', "caf\u00e9"]
+    assert flowedge_amd.weights_digest(str(path)) == fingerprint.fingerprint(str(path))
+
+
+def test_header_reader_rejects_malformed_json(tmp_path):
+    import struct
+    good = b'{"w":{"dtype":"F32","shape":[1],"data_offsets":[0,4]}}'
+    for bad in (b'{"w":{"dtype":"F32","shape":[1],"data_offsets":[0,4]}',  # unclosed
+                b'{"w":{"dtype":"F32","shape":[1],"data_offsets":[0,4]},}',  # trailing comma
+                b'{"w\\x":{"dtype":"F32","shape":[1],"data_offsets":[0,4]}}',  # bad escape
+                b'{"w":{"dtype":"F32","shape":[1,],"data_offsets":[0,4]}}',  # bad list
+                b'{"w":{"dtype":"F32","shape":[1],"data_offsets":[0,8]}}'):  # out of bounds
+        for body, ok in ((good, True), (bad, False)):
+            path = tmp_path / "h.safetensors"
+            with open(path, "wb") as f:
+                f.write(struct.pack("<Q", len(body)) + body + b"\0\0\0\0")
+            w = flowedge_amd.lib().fe_weights_load(str(path).encode())
+            assert bool(w) == ok, (body, flowedge_amd.last_error())
+            if w:
+                flowedge_amd.lib().fe_weights_free(w)
+            else:
+                assert flowedge_amd.last_error() != ""
+
+
 def test_fingerprint_sensitivity(tmp_path):
     # core_model_tests.cc:392-393: equal inputs give equal digests, any change another digest.
     import numpy as np

@@ -115,6 +115,65 @@ def test_no_device_allocation_after_load(tiny_engine):
     assert flowedge_amd.device_alloc_count() == before
 
 
+def test_no_allocation_or_capture_after_first_call(tiny):
+    # After the first call of a shape (or fe_engine_prepare) its sampling calls capture no graph
+    # and leave the device's free memory unchanged (nothing allocated by the library or by the
+    # HIP runtime on its behalf).
+    import torch
+
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec, batch=6)
+    with flowedge_amd.Engine(tiny) as e:
+        e.prepare(0, 6, 10, 0)
+        e.sample_diffusion(cond[0], noise[0], steps=10)
+        e.sample_diffusion(cond[0], noise[0], steps=10, scheduler="ddpm", seed=3)
+        e.sample_diffusion_batch(cond, noise, steps=10)
+        e.diffusion_denoise(cond[0], noise[0], 7.0)
+        captures = e.graph_captures
+        assert captures == 3
+        allocs = flowedge_amd.device_alloc_count()
+        free0 = torch.cuda.mem_get_info()[0]
+        for _ in range(3):
+            e.sample_diffusion(cond[0], noise[0], steps=10)
+            e.sample_diffusion(cond[0], noise[0], steps=10, scheduler="ddpm", seed=3)
+            e.sample_diffusion_batch(cond, noise, steps=10)
+            e.diffusion_denoise(cond[0], noise[0], 7.0)
+        assert e.graph_captures == captures
+        assert flowedge_amd.device_alloc_count() == allocs
+        assert torch.cuda.mem_get_info()[0] == free0
+
+
+def test_diagnostics_then_first_sample(tiny, tiny_oracle):
+    # Convolution diagnostics (listing and timing) before the first sampling graph of a fresh
+    # engine: the graph is captured afterwards and matches the oracle.
+    spec = ck.SPECS["tiny"]
+    cond, noise = ck.inputs(spec)
+    with flowedge_amd.Engine(tiny) as e:
+        convs = e.convolutions()
+        assert len(convs) == 29
+        assert e.time_convolutions([c["index"] for c in convs], batch=1, iters=2) > 0
+        assert e.graph_captures == 0
+        got = e.sample_diffusion(cond[0], noise[0], steps=10)
+        assert e.graph_captures == 1
+    assert maxerr(got, tiny_oracle.sample(cond[0], noise[0], 10)) <= TOL
+
+
+def test_denoise_rejects_velocity_model(ckpt_dir):
+    # engine_runtime.cc:476-479: no Diffusion Policy (epsilon) head -> status 4.
+    spec = ck.UNetSpec(dims=(64, 128, 256), action_dim=7, cond_dim=32, prediction=1)
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, "flow_small_gpu.safetensors"), spec)
+    cond, x = ck.inputs(spec)
+    with flowedge_amd.Engine(path) as e:
+        lib = flowedge_amd.lib()
+        p = flowedge_amd._p
+        c, n = np.ascontiguousarray(cond[0]), np.ascontiguousarray(x[0])
+        out = np.empty((spec.horizon, spec.action_dim), np.float32)
+        assert lib.fe_engine_diffusion_denoise(e._h, p(c), p(n), 5.0, p(out)) == 4
+        assert flowedge_amd.last_error() == "Model has no Diffusion Policy head"
+        with pytest.raises(RuntimeError):
+            e.sample_condition(cond[0], x[0], np.empty(3, np.float32), steps=2)
+
+
 def test_status_codes(tiny_engine, tiny):
     lib = flowedge_amd.lib()
     spec = ck.SPECS["tiny"]
@@ -387,4 +446,50 @@ def test_flow_batched_mfma(ckpt_dir):
         got = e.sample_condition_batch(cond, x0, steps=4, method="rk4")
     err = maxerr(got, o.sample_batch(cond, x0, 4, 1, flowedge_amd.SOLVERS["rk4"], workers=8))
     say(f"flow batch={B} max err {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("steps", [1, 3, 10])
+def test_ddpm_closed_form_constant_epsilon(ckpt_dir, steps):
+    # The device DDPM step and noise stream against the float64 closed form of
+    # diffusion.cc:1005-1024 on a model whose epsilon is its output bias, at batch 1 and on the
+    # matrix cores (batch 9: every sample draws the same stream, as 9 independent calls).
+    spec = ck.SPECS["tiny"]
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, "tiny_zero_out.safetensors"), spec,
+                                  zero=("dp.f.o.w",))
+    bias = ck.read_safetensors(path)["dp.f.o.b"]
+    eps = np.tile(bias, (spec.horizon, 1))
+    cond, noise = ck.inputs(spec, batch=9)
+    say(f"DDPM closed form steps={steps}")
+    with flowedge_amd.Engine(path) as e:
+        for seed in (0, 42):
+            for scale in (1.0, 0.05):
+                x = noise * np.float32(scale)
+                ref = unet_ref.ddpm_const_eps(x[0], eps, steps, 100, 1.0, -1.0, 1.0, seed)
+                got = e.sample_diffusion(cond[0], x[0], steps=steps, scheduler="ddpm", seed=seed)
+                assert maxerr(got, ref) <= 3e-5
+                batch = e.sample_diffusion_batch(cond, x, steps=steps, scheduler="ddpm",
+                                                 seed=seed)
+                for b in (0, 4, 8):
+                    want = unet_ref.ddpm_const_eps(x[b], eps, steps, 100, 1.0, -1.0, 1.0, seed)
+                    assert maxerr(batch[b], want) <= 3e-5
+
+
+@pytest.mark.parametrize("workload,batch", [("tiny", 1), ("tiny", 9), ("pusht", 1), ("pusht", 8)])
+def test_converter_bf16_linear_layout(ckpt_dir, workload, batch):
+    # The reference converter's --dtype bf16 layout: BF16 2-D linears (time MLP, FiLM), F32
+    # convolutions.  Loaded through the C ABI and held to the oracle on the same file at the fp32
+    # bound (the convolutions are F32; the BF16 linears are widened identically by both).
+    import dataclasses
+    spec = dataclasses.replace(ck.SPECS[workload], bf16_linears=True)
+    path = os.path.join(ckpt_dir, f"{workload}_bf16_linears.safetensors")
+    if not os.path.exists(path):
+        ck.write_synthetic(path, spec)
+    cond, noise = ck.inputs(spec, batch=batch)
+    say(f"{workload} converter BF16-linear layout B={batch}")
+    with flowedge_amd.Engine(path) as e:
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+    want = oracle.Oracle(path).sample_batch(cond, noise, 10, workers=16)
+    err = maxerr(got, want)
+    say(f"{workload} BF16-linear layout B={batch} max err {err:.3e}")
     assert err <= TOL

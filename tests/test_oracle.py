@@ -216,6 +216,26 @@ def test_denoise_matches_float64_torch_unet_reference_fixture(fixture_ckpt):
     assert np.abs(o.denoise(other, sample, 7.0) - eps).sum() > 0
 
 
+def test_converter_bf16_linear_layout(ckpt_dir):
+    # The reference converter's --dtype bf16 layout (convert.py:602-610): 2-D linear weights in
+    # BF16, convolutions, biases and norms in F32 (diffusion.cc:656-660, 678-683 widen the BF16
+    # linears).  The oracle reads it and matches the float64 U-Net on the widened values.
+    import dataclasses
+    spec = dataclasses.replace(ck.SPECS["tiny"], bf16_linears=True)
+    path = ck.write_synthetic(os.path.join(ckpt_dir, "tiny_bf16_linears.safetensors"), spec)
+    tensors = ck.read_safetensors(path)
+    bf16 = sorted(k for k, v in tensors.items() if v.dtype == np.uint16)
+    assert bf16 and all(tensors[k].ndim == 2 for k in bf16)
+    assert all(tensors[k].dtype == np.float32 for k in tensors if k.endswith(".w") and
+               tensors[k].ndim == 3)
+    o = oracle.Oracle(path)
+    cond, noise = ck.inputs(spec)
+    for t in (99.0, 20.0):
+        eps = o.denoise(cond[0], noise[0], t)
+        ref = unet_ref.torch_unet_eps(tensors, cond[0], noise[0], t)
+        np.testing.assert_allclose(eps, ref, atol=2e-5, rtol=0)
+
+
 def test_sampler_invariants_reference_fixture(fixture_ckpt):
     # core_model_tests.cc:441-472.
     o = oracle.Oracle(fixture_ckpt)
@@ -250,6 +270,67 @@ def test_zero_output_conv_gives_bias_and_closed_form_ddim(ckpt_dir):
     # clip_sample: the last step returns clip(x0), so actions stay inside [min, max].
     got = o.sample(cond[0], noise[0] * 50, 10, 0, 0)
     assert np.all(got >= -1.0) and np.all(got <= 1.0)
+
+
+@pytest.mark.parametrize("steps", [1, 3, 10])
+@pytest.mark.parametrize("seed", [0, 42])
+def test_ddpm_closed_form_on_constant_epsilon(ckpt_dir, steps, seed):
+    # DDPM posterior step (diffusion.cc:1005-1024) against an independent float64 restatement on a
+    # model whose epsilon is its output bias at every step.  Inputs scaled so that x0 stays
+    # inside the clip range on some steps and is clipped on others.
+    spec = ck.SPECS["tiny"]
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, "tiny_zero_out.safetensors"), spec,
+                                  zero=("dp.f.o.w",))
+    o = oracle.Oracle(path)
+    bias = ck.read_safetensors(path)["dp.f.o.b"]
+    cond, noise = ck.inputs(spec)
+    for scale in (1.0, 0.05):
+        x = noise[0] * np.float32(scale)
+        got = o.sample(cond[0], x, steps, 1, seed)
+        ref = unet_ref.ddpm_const_eps(x, np.tile(bias, (spec.horizon, 1)), steps, 100, 1.0,
+                                      -1.0, 1.0, seed)
+        np.testing.assert_allclose(got, ref, atol=3e-5, rtol=0,
+                                   err_msg=f"steps={steps} seed={seed} scale={scale}")
+
+
+def test_ddpm_closed_form_rejects_plausible_mistakes(ckpt_dir):
+    # The closed form above separates the DDPM step from its likely mistakes: swapped posterior
+    # coefficients, a variance without the (1 - abar_p) / (1 - abar_t) factor, and a noise stream
+    # shifted by one state (a draw on the last step instead of the first).
+    spec = ck.SPECS["tiny"]
+    path = unet_ref.write_variant(os.path.join(ckpt_dir, "tiny_zero_out.safetensors"), spec,
+                                  zero=("dp.f.o.w",))
+    o = oracle.Oracle(path)
+    e = np.tile(ck.read_safetensors(path)["dp.f.o.b"], (spec.horizon, 1)).astype(np.float64)
+    cond, noise = ck.inputs(spec)
+    x_in = noise[0] * np.float32(0.05)
+    got = o.sample(cond[0], x_in, 10, 1, 7).astype(np.float64)
+    ac = unet_ref.alphas_cumprod_f64(100)
+    z = ck.gaussian(7, 10 * e.size).astype(np.float64)
+
+    def run(swap=False, plain_var=False, shift=0):
+        x = x_in.astype(np.float64)
+        for i in range(10):
+            ts = (9 - i) * 10
+            prev = ts - 10
+            at = ac[ts]
+            ap = ac[prev] if prev >= 0 else 1.0
+            x0 = np.clip((x - np.sqrt(1 - at) * e) / np.sqrt(at), -1, 1)
+            beta = 1 - at / ap
+            c0 = np.sqrt(ap) * beta / (1 - at)
+            c1 = np.sqrt(at / ap) * (1 - ap) / (1 - at)
+            if swap:
+                c0, c1 = c1, c0
+            var = beta if plain_var else (1 - ap) / (1 - at) * beta
+            draw = (prev >= 0) if shift == 0 else (i > 0)
+            k = i - (1 if shift else 0)
+            x = c0 * x0 + c1 * x + (np.sqrt(var) * z[k * e.size:(k + 1) * e.size].reshape(e.shape)
+                                    if draw else 0.0)
+        return x
+
+    assert np.max(np.abs(run() - got)) <= 3e-5
+    for wrong in (run(swap=True), run(plain_var=True), run(shift=1)):
+        assert np.max(np.abs(wrong - got)) > 1e-3
 
 
 def test_partial_sampling_closed_form(ckpt_dir):

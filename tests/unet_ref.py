@@ -184,6 +184,43 @@ def ddim_const_eps(noise, eps_const, steps: int, T: int, clip: float | None, ami
     return (x + 1) * 0.5 * (np.asarray(amax) - np.asarray(amin)) + np.asarray(amin)
 
 
+def ddpm_const_eps(noise, eps_const, steps: int, T: int, clip: float | None, amin, amax,
+                   seed: int):
+    """DDPM posterior sampling (diffusers DDPMScheduler.step without variance clipping) with an
+    epsilon that is the same at every step, in float64.
+
+    x_prev = c0 clip(x0) + c1 x + sigma z with abar_t, abar_p = abar at t and t - T/steps (1 once
+    negative), alpha = abar_t / abar_p, beta = 1 - alpha:
+        c0 = sqrt(abar_p) beta / (1 - abar_t),  c1 = sqrt(alpha) (1 - abar_p) / (1 - abar_t),
+        sigma^2 = (1 - abar_p) / (1 - abar_t) beta.
+    z is the seeded Gaussian stream; it advances only on steps that add noise (every step but
+    the last), one value per state entry in [t][a] order.
+    """
+    ac = alphas_cumprod_f64(T)
+    x = np.asarray(noise, np.float64).copy()
+    e = np.asarray(eps_const, np.float64)
+    ratio = T // steps
+    z = ck.gaussian(seed, max(steps - 1, 1) * x.size).astype(np.float64)
+    drawn = 0
+    for i in range(steps):
+        ts = (steps - 1 - i) * ratio
+        prev = ts - ratio
+        at = ac[ts]
+        ap = ac[prev] if prev >= 0 else 1.0
+        x0 = (x - math.sqrt(1 - at) * e) / math.sqrt(at)
+        if clip is not None:
+            x0 = np.clip(x0, -clip, clip)
+        alpha = at / ap
+        beta = 1.0 - alpha
+        nxt = math.sqrt(ap) * beta / (1 - at) * x0 + math.sqrt(alpha) * (1 - ap) / (1 - at) * x
+        if prev >= 0:
+            sigma = math.sqrt((1 - ap) / (1 - at) * beta)
+            nxt = nxt + sigma * z[drawn:drawn + x.size].reshape(x.shape)
+            drawn += x.size
+        x = nxt
+    return (x + 1) * 0.5 * (np.asarray(amax) - np.asarray(amin)) + np.asarray(amin)
+
+
 # Shapes the checkpoint format admits beyond the common U-Net configurations: odd kernel sizes
 # other than 3 and 5 (including 1), horizons that are not powers of two, more than 32 groups,
 # widths that are not multiples of 16, width * length above 8192, more than 64 action dims and a
