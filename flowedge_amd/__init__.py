@@ -38,6 +38,7 @@ EXPORTS = [
     "fe_engine_flow_action_metadata", "fe_engine_diffusion_begin",
     "fe_engine_diffusion_begin_generation", "fe_engine_diffusion_advance",
     "fe_weights_model_digest", "fe_engine_conv_path", "fe_engine_graph_captures",
+    "fe_engine_diffusion_denoise_noalloc",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -124,6 +125,7 @@ def lib():
     L.fe_engine_diffusion_denoise_batch.argtypes = [vp, _f32p, _f32p, sz, ctypes.c_float, _f32p]
     L.fe_engine_sample_device.argtypes = [vp, cint, vp, vp, sz, sz, cint, u64, vp]
     L.fe_engine_prepare.argtypes = [vp, cint, sz, sz, cint]
+    L.fe_engine_diffusion_denoise_noalloc.argtypes = [vp, vp, vp, sz, ctypes.c_float, vp, vp]
     L.fe_device_alloc_count.restype = u64
     L.fe_engine_graph_captures.restype = u64
     L.fe_engine_graph_captures.argtypes = [vp]
@@ -425,6 +427,13 @@ class Engine:
         """Device-resident sampling: the pointers are device addresses (e.g. tensor.data_ptr())."""
         self._check(lib().fe_engine_sample_device(self._h, kind, cond_ptr, noise_ptr, batch,
                                                   steps, mode, seed, action_ptr))
+
+    def denoise_noalloc(self, cond_ptr: int, sample_ptr: int, batch: int, timestep: float,
+                        out_ptr: int, stream: int | None = None) -> None:
+        """Allocation-free batched denoise on device pointers (static device scratch); with
+        `stream` (a hipStream_t handle) it is only enqueued."""
+        self._check(lib().fe_engine_diffusion_denoise_noalloc(
+            self._h, cond_ptr, sample_ptr, batch, float(timestep), out_ptr, stream))
 
     def prepare(self, kind: int, batch: int, steps: int, mode: int) -> None:
         self._check(lib().fe_engine_prepare(self._h, kind, batch, steps, mode))

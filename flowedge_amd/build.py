@@ -19,7 +19,7 @@ OBJDIR = os.path.join(HERE, "_build")
 SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/conv_fused.hip",
            "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip",
            "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/conv_general.hip",
-           "csrc/identity.cpp"]
+           "csrc/identity.cpp", "csrc/scratch.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -183,7 +183,8 @@ constexpr std::size_t kMaxBlocks = 4 * kMaxStages + 2;
 
 // Per-call device buffers (the reference's WorkspacePlan, diffusion.cc:90-126,283-381): byte
 // offsets from a workspace base, planned for a batch size and a number of FiLM time rows.  The
-// engine's arena holds one Work for its max batch.
+// engine's arena holds one Work for its max batch; the allocation-free denoise entry point plans
+// another one inside the library's static scratch array.
 struct Work {
   std::size_t size = 0;
   std::size_t batch = 0, film_rows = 0, splitk_floats = 0;
@@ -229,6 +230,9 @@ struct FeEngine {
   std::size_t arena_bytes = 0;
   char* ws = nullptr;  // workspace base of `w`
   Work w;
+  // This device's static scratch array (allocation-free entry point), set up at load.
+  void* scratch = nullptr;
+  hipError_t scratch_status = hipErrorNotInitialized;
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = -1.0f;
@@ -1616,6 +1620,9 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     hip_fail("hipGetDevice", st);
     return nullptr;
   }
+  // Device address of this GPU's static scratch array (used only by the allocation-free entry
+  // point, which reports a failure here when it is called).
+  e->scratch_status = fe::hip::scratch_setup(e->device, &e->scratch);
   if (env_flag("FLOWEDGE_HIP_FAIL_ALLOC")) {
     set_error("Device arena allocation failed (FLOWEDGE_HIP_FAIL_ALLOC=1)");
     return nullptr;
@@ -1932,6 +1939,67 @@ int fe_engine_diffusion_denoise(fe_engine* engine, const float* condition,
                                 float* predicted_noise) {
   return fe_engine_diffusion_denoise_batch(engine, condition, normalized_sample, 1, timestep,
                                            predicted_noise);
+}
+
+int fe_engine_diffusion_denoise_noalloc(fe_engine* engine, const float* condition_dev,
+                                        const float* sample_dev, size_t batch, float timestep,
+                                        float* predicted_noise_dev, void* stream) {
+  clear_error();
+  if (engine == nullptr || condition_dev == nullptr || sample_dev == nullptr ||
+      predicted_noise_dev == nullptr || !std::isfinite(timestep) || batch == 0 ||
+      batch > 65535) {
+    set_error("Invalid arguments to fe_engine_diffusion_denoise_noalloc");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  FeEngine* e = engine;
+  if (e->cfg.prediction != 0) {
+    set_error("Model has no Diffusion Policy head");
+    return FE_STATUS_UNSUPPORTED_MODEL;
+  }
+  if (e->scratch == nullptr) {
+    return hip_fail("Device scratch of the allocation-free entry point is unavailable",
+                    e->scratch_status);
+  }
+  // The whole workspace of one evaluation of `batch` samples lives in the scratch array; what is
+  // left of it holds split-K partials (fewer partials only means fewer K splits).
+  Work w = plan_work(*e, batch, 1, 0);
+  const std::size_t base = (w.size + kAlign - 1) / kAlign * kAlign;
+  if (w.size > fe::hip::kScratchBytes) {
+    set_error("Batch too large for the allocation-free scratch: " + std::to_string(w.size) +
+              " bytes needed, " + std::to_string(fe::hip::kScratchBytes) + " available");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const std::size_t spare = fe::hip::kScratchBytes > base ? fe::hip::kScratchBytes - base : 0;
+  w = plan_work(*e, batch, 1, std::min(kSplitKFloats, spare / 4));
+  hipError_t st = hipSetDevice(e->device);
+  if (st != hipSuccess) return hip_fail("hipSetDevice", st);
+  // Enqueue one evaluation against the scratch workspace on the caller's stream (or the engine's);
+  // the engine's own workspace and any resumable solve are left untouched.
+  char* const saved_ws = e->ws;
+  const Work saved_w = e->w;
+  const hipStream_t saved_stream = e->stream;
+  e->ws = static_cast<char*>(e->scratch);
+  e->w = w;
+  if (stream != nullptr) e->stream = static_cast<hipStream_t>(stream);
+  using namespace fe::hip;
+  const int b = static_cast<int>(batch);
+  TimeSpec ts;
+  ts.mode = kTimesSingle;
+  ts.t0 = timestep;
+  UpdateOp u{};
+  u.kind = kUpdateDenoise;
+  u.out = predicted_noise_dev;
+  st = begin_sample(sample_dev, e->wp(e->w.x_in), e->wp(e->w.x_in), b,
+                    static_cast<int>(e->cfg.horizon), static_cast<int>(e->cfg.action_dim),
+                    e->stream);
+  if (st == hipSuccess) st = enqueue_film(*e, ts, 1, b, condition_dev);
+  if (st == hipSuccess) st = enqueue_unet(*e, b, e->wp(e->w.film_table), u);
+  e->ws = saved_ws;
+  e->w = saved_w;
+  e->stream = saved_stream;
+  if (st == hipSuccess && stream == nullptr) st = hipStreamSynchronize(e->stream);
+  if (st != hipSuccess) return hip_fail("Diffusion denoiser execution failed", st);
+  return FE_STATUS_OK;
 }
 
 int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_dev,

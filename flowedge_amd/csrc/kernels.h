@@ -185,5 +185,10 @@ hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
 hipError_t finish_sample(const float* x, const float* amin, const float* amax, float* action,
                          int batch, int horizon, int action_dim, hipStream_t stream);
 
+// Static device scratch of the allocation-free entry point (scratch.hip): kScratchBytes per GPU.
+// scratch_setup returns the array's device address on `device`, which must be the current device;
+// the address is looked up once per device and kept.
+constexpr std::size_t kScratchBytes = std::size_t{32} << 20;
+hipError_t scratch_setup(int device, void** ptr);
 
 }  // namespace fe::hip

@@ -287,6 +287,22 @@ int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_
                             const float* noise_dev, size_t batch, size_t steps, int mode,
                             uint64_t seed, float* action_dev);
 
+/* Allocation-free batched denoise.  No counterpart in the reference: for callers that cannot
+ * allocate device memory during the call -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  The same U-Net evaluation as fe_engine_diffusion_denoise_batch
+ * on device pointers (condition [batch][condition_dim], normalized_sample and predicted_noise
+ * [batch][horizon][action_dim]), with every intermediate buffer inside the library's static
+ * device scratch array (32 MiB per GPU, held until the process ends): no hipMalloc, no graph
+ * capture, no allocating library call.  A batch whose buffers exceed the scratch array returns
+ * status 1 before anything is enqueued (pusht-size U-Net: about 1.5 MiB per sample).  `stream` is a
+ * hipStream_t to enqueue on, returning at once (capturable); NULL uses the engine's stream and
+ * returns when the result is written.  Every call on one GPU shares that GPU's scratch array,
+ * so calls that overlap on one GPU (other streams, other engines) race; calls on one stream are
+ * ordered.  The engine's own workspace and any resumable solve are not touched. */
+int fe_engine_diffusion_denoise_noalloc(fe_engine* engine, const float* condition_dev,
+                                        const float* normalized_sample_dev, size_t batch,
+                                        float timestep, float* predicted_noise_dev, void* stream);
+
 /* Build (capture and instantiate) the sampling graph for this shape ahead of the first call.
  * A sampling call of a (kind, batch, steps, mode) with no cached graph captures one itself
  * (HIP-runtime host and kernel-argument allocations, about a millisecond); the engine keeps the
