@@ -38,7 +38,8 @@ EXPORTS = [
     "fe_engine_flow_action_metadata", "fe_engine_diffusion_begin",
     "fe_engine_diffusion_begin_generation", "fe_engine_diffusion_advance",
     "fe_weights_model_digest", "fe_engine_conv_path", "fe_engine_graph_captures",
-    "fe_engine_diffusion_denoise_noalloc",
+    "fe_engine_diffusion_denoise_noalloc", "fe_engine_persistent_tick",
+    "fe_engine_persistent_tick_reason",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -129,6 +130,9 @@ def lib():
     L.fe_device_alloc_count.restype = u64
     L.fe_engine_graph_captures.restype = u64
     L.fe_engine_graph_captures.argtypes = [vp]
+    L.fe_engine_persistent_tick.argtypes = [vp]
+    L.fe_engine_persistent_tick_reason.restype = ctypes.c_char_p
+    L.fe_engine_persistent_tick_reason.argtypes = [vp]
     L.fe_engine_last_device_ms.restype = ctypes.c_float
     L.fe_engine_last_device_ms.argtypes = [vp]
     L.fe_engine_conv_count.argtypes = [vp, ctypes.POINTER(sz)]
@@ -268,6 +272,15 @@ class Engine:
     @property
     def device_bytes(self) -> int:
         return int(lib().fe_engine_device_bytes(self._h))
+
+    @property
+    def persistent_tick(self) -> bool:
+        """Batch-1 ticks run as one persistent kernel launch (else per-layer graphs)."""
+        return bool(lib().fe_engine_persistent_tick(self._h))
+
+    @property
+    def persistent_tick_reason(self) -> str:
+        return lib().fe_engine_persistent_tick_reason(self._h).decode()
 
     @property
     def graph_captures(self) -> int:

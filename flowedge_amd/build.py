@@ -19,9 +19,13 @@ OBJDIR = os.path.join(HERE, "_build")
 SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/conv_fused.hip",
            "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip",
            "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/conv_general.hip",
-           "csrc/identity.cpp", "csrc/scratch.hip"]
+           "csrc/identity.cpp", "csrc/scratch.hip", "csrc/chain.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+# -ffp-contract=on: a multiply and an add fuse only within one expression, so a kernel body
+# rounds the same way in every kernel it is inlined into (the persistent tick kernel and the
+# per-layer kernels give bit-identical results); "fast" would also fuse across statements
+# wherever the surrounding code places both in one basic block.
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=on",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", os.path.join(ROOT, "include")]
 

@@ -105,16 +105,19 @@ bool conv_fused_supported(const ConvOp& op, const ConvOp* res1x1, const ConvInpu
   return fused_plan(op, res1x1, in, yr, batch, p);
 }
 
-hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
-                      View yr, int batch, hipStream_t stream) {
+namespace conv {
+
+bool fused_args(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y, View yr,
+                int batch, Args& a, int& vec, int& pro) {
   const bool res = res1x1 != nullptr;
   LaunchPlan p;
-  if (!fused_plan(op, res1x1, in, yr, batch, p)) return hipErrorInvalidValue;
-  const int pro = prologue_of(in);
+  if (!fused_plan(op, res1x1, in, yr, batch, p)) return false;
+  pro = prologue_of(in);
+  vec = p.vec;
   const std::uint64_t wbytes = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
   const std::uint64_t rwbytes =
       res ? static_cast<std::uint64_t>(op.oc) * op.ic * (res1x1->bf16 ? 2 : 4) : 0;
-  Args a{};
+  a = Args{};
   a.wbytes = static_cast<unsigned>(wbytes);
   a.rwbytes = static_cast<unsigned>(rwbytes);
   a.w = op.w;
@@ -136,9 +139,20 @@ hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& i
   a.tpr = p.tpr;
   a.nch = p.nch;
   a.in = in;
+  return true;
+}
+
+}  // namespace conv
+
+hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
+                      View yr, int batch, hipStream_t stream) {
+  const bool res = res1x1 != nullptr;
+  Args a;
+  int vec = 4, pro = 0;
+  if (!conv::fused_args(op, res1x1, in, y, yr, batch, a, vec, pro)) return hipErrorInvalidValue;
   if (op.mode == kConvSame)
-    return op.k == 5 ? launch_same5(op.lin, p.vec, pro, res, a, batch, stream)
-                     : launch_same3(op.lin, p.vec, pro, res, a, batch, stream);
+    return op.k == 5 ? launch_same5(op.lin, vec, pro, res, a, batch, stream)
+                     : launch_same3(op.lin, vec, pro, res, a, batch, stream);
   return launch_resample(op.mode, op.lin, pro, a, batch, stream);
 }
 

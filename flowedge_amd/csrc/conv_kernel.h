@@ -92,6 +92,13 @@ struct Args {
   ConvInput in;
 };
 
+// Per-launch replacements of two input pointers (the persistent tick kernel runs one step table
+// for every evaluation): the FiLM time row of the evaluation and a per-workgroup input.
+struct Override {
+  const float* src = nullptr;        // replaces in.src when set
+  const float* film_time = nullptr;  // replaces in.film_time when set
+};
+
 // Workgroup barrier that orders LDS accesses only: global loads in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { __barrier(__CLK_LOCAL_MEM_FENCE); }
 
@@ -229,22 +236,65 @@ struct StageRegs {
   float tb[PRO == kProFilm ? QP : 1], cb[PRO == kProFilm ? QP : 1];
 };
 
+// The per-channel prologue parameters of chunk q (GroupNorm affine, FiLM time and condition rows;
+// one channel per chunk at LIN >= 4): tensors no step of a tick writes.
+template <int LIN, int PRO>
+__device__ __forceinline__ void stage_chunk_params(const Args& a, int b, StageRegs<LIN, PRO>& s,
+                                                   Override ov, int m, int q) {
+  if constexpr (PRO != kProPlain && LIN >= 4) {
+    const ConvInput& in = a.in;
+    const int c = 4 * q / LIN;
+    s.gam[m] = in.gamma[c];
+    s.bet[m] = in.beta[c];
+    if constexpr (PRO == kProFilm) {
+      const float* ft = (ov.film_time != nullptr ? ov.film_time : in.film_time) + in.film_off;
+      const float* fc = in.film_cond + b * in.film_cond_stride + in.film_off;
+      s.ts[m] = ft[c];
+      s.cs[m] = fc[c];
+      s.tb[m] = ft[in.split + c];
+      s.cb[m] = fc[in.split + c];
+    }
+  }
+}
+
+// The tick kernel's early half of step 1: the parameters, requested before it waits for the
+// producers of the input.
+template <int LIN, int PRO>
+__device__ __forceinline__ void stage_params(const Args& a, int b, StageRegs<LIN, PRO>& s,
+                                             Override ov) {
+  using S = StageRegs<LIN, PRO>;
+  if constexpr (PRO != kProPlain && LIN >= 4) {
+    const int nqn = a.in.split * LIN / 4;
+#pragma unroll
+    for (int m = 0; m < S::QN; ++m) {
+      const int q = threadIdx.x + m * kThreads;
+      if (q < nqn) stage_chunk_params<LIN, PRO>(a, b, s, ov, m, q);
+    }
+  }
+}
+
 // Step 1: every global read of the prologue, issued before any weight load.  Lane `tid` takes the
 // float4 chunks q = tid + m * kThreads of the flat [C][L] input; chunks q < nqn come from `src`.
-template <int LIN, int PRO>
-__device__ __forceinline__ void stage_issue(const Args& a, int b, StageRegs<LIN, PRO>& s) {
+// CHAIN (persistent tick kernel): activations written by other workgroups of the same launch are
+// read device-coherently, and the parameters were requested by stage_params.
+template <int LIN, int PRO, bool CHAIN>
+__device__ __forceinline__ void stage_issue(const Args& a, int b, StageRegs<LIN, PRO>& s,
+                                            Override ov) {
   using S = StageRegs<LIN, PRO>;
   const ConvInput& in = a.in;
   const int nq = a.ic * LIN / 4;
   const int nqn = in.split * LIN / 4;
   const int tid = threadIdx.x;
-  const float* src = in.src + b * in.src_stride;
+  const float* src = (ov.src != nullptr ? ov.src : in.src) + b * in.src_stride;
+  const float* plain = in.plain != nullptr ? in.plain + b * in.plain_stride : src;
 #pragma unroll
   for (int m = 0; m < S::QMAX; ++m) {
     const int q = tid + m * kThreads;
     s.x[m] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (q < nq) {
-      const float* p = q < nqn ? src + 4 * q : in.plain + b * in.plain_stride + 4 * (q - nqn);
+    if constexpr (CHAIN) {
+      if (q < nq) s.x[m] = ld4_dev(q < nqn ? src + 4 * q : plain + 4 * (q - nqn));
+    } else if (q < nq) {
+      const float* p = q < nqn ? src + 4 * q : plain + 4 * (q - nqn);
       s.x[m] = *reinterpret_cast<const float4*>(p);
     }
   }
@@ -253,21 +303,13 @@ __device__ __forceinline__ void stage_issue(const Args& a, int b, StageRegs<LIN,
     for (int m = 0; m < S::QN; ++m) {
       const int q = tid + m * kThreads;
       if (q < nqn) {
-        if constexpr (PRO == kProResid)
-          s.r[m] = *reinterpret_cast<const float4*>(in.res + b * in.res_stride + 4 * q);
-        if constexpr (LIN >= 4) {
-          const int c = 4 * q / LIN;
-          s.gam[m] = in.gamma[c];
-          s.bet[m] = in.beta[c];
-          if constexpr (PRO == kProFilm) {
-            const float* ft = in.film_time + in.film_off;
-            const float* fc = in.film_cond + b * in.film_cond_stride + in.film_off;
-            s.ts[m] = ft[c];
-            s.cs[m] = fc[c];
-            s.tb[m] = ft[in.split + c];
-            s.cb[m] = fc[in.split + c];
-          }
+        if constexpr (PRO == kProResid) {
+          if constexpr (CHAIN)
+            s.r[m] = ld4_dev(in.res + b * in.res_stride + 4 * q);
+          else
+            s.r[m] = *reinterpret_cast<const float4*>(in.res + b * in.res_stride + 4 * q);
         }
+        if constexpr (!CHAIN) stage_chunk_params<LIN, PRO>(a, b, s, ov, m, q);
       }
     }
   }
@@ -290,9 +332,9 @@ __device__ __forceinline__ void write_chunk(float* xs, int nv, int q, float4 v) 
 }
 
 // Steps 3: statistics, transform, materialisation and LDS staging.  Called by every lane.
-template <int LIN, int PRO>
+template <int LIN, int PRO, bool CHAIN>
 __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, StageRegs<LIN, PRO>& s,
-                                             float* xs, float* gmean, float* ginv) {
+                                             float* xs, float* gmean, float* ginv, Override ov) {
   using S = StageRegs<LIN, PRO>;
   const ConvInput& in = a.in;
   const int nq = a.ic * LIN / 4;
@@ -301,12 +343,25 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
   if constexpr (PRO != kProPlain) {
     const int nqn = in.split * LIN / 4;
     const int npg = in.split / in.groups * LIN / 4;  // chunks per group
-    // fp64 partial sums per chunk, aliased over xs (written only after the next two barriers).
+    // fp64 partial sums, aliased over xs (written only after the next two barriers).
     double* ps = reinterpret_cast<double*>(xs);
+    // Mean and 1/std of group g from its sums over n = 4 npg values.
+    auto finish = [&](int g, double sum, double sq) {
+      const double n = 4.0 * npg;
+      const double mean = sum / n;
+      const double var = fmax(0.0, sq / n - mean * mean);
+      gmean[g] = static_cast<float>(mean);
+      ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
+    };
+    int gq[S::QN];  // group of chunk tid + m * kThreads
+    // One fp64 partial pair per chunk; sixteen lanes per group, all kMaxGroups groups in one
+    // pass, each lane summing every 16th partial of its group before a 16-lane row reduction
+    // (DPP), and the row's first lane finishes the group.
     double* pq = ps + nqn;
 #pragma unroll
     for (int m = 0; m < S::QN; ++m) {
       const int q = tid + m * kThreads;
+      gq[m] = q / npg;
       if (q < nqn) {
         const double d0 = s.x[m].x, d1 = s.x[m].y, d2 = s.x[m].z, d3 = s.x[m].w;
         ps[q] = (d0 + d1) + (d2 + d3);
@@ -314,9 +369,6 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
       }
     }
     lds_barrier();
-    // Sixteen lanes per group, all kMaxGroups groups in one pass: each lane sums every 16th
-    // partial of its group, a 16-lane row reduction (DPP) completes the group, and the row's
-    // first lane finishes the mean and 1/std.
     static_assert(kThreads / 16 >= kMaxGroups, "one 16-lane row per group");
     {
       const int g = tid >> 4, sub = tid & 15;
@@ -329,22 +381,22 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
       }
       sum = row_sum(sum);
       sq = row_sum(sq);
-      if (sub == 0 && g < in.groups) {
-        const double n = 4.0 * npg;
-        const double mean = sum / n;
-        const double var = fmax(0.0, sq / n - mean * mean);
-        gmean[g] = static_cast<float>(mean);
-        ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
-      }
+      if (sub == 0 && g < in.groups) finish(g, sum, sq);
     }
     lds_barrier();  // statistics visible; the partials are no longer read
-    const float* ft = PRO == kProFilm ? in.film_time + in.film_off : nullptr;
+    const float* ft =
+        PRO == kProFilm
+            ? (ov.film_time != nullptr ? ov.film_time : in.film_time) + in.film_off
+            : nullptr;
     const float* fc = PRO == kProFilm ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
+    // Workgroup wg materialises the chunks q with q % blocks == wg; r tracks q % blocks.
+    int r = in.mat != nullptr ? tid % a.blocks : 0;
+    const int rstep = in.mat != nullptr ? kThreads % a.blocks : 0;
 #pragma unroll
     for (int m = 0; m < S::QN; ++m) {
       const int q = tid + m * kThreads;
       if (q < nqn) {
-        const int g = q / npg;
+        const int g = gq[m];
         const float mean = gmean[g], inv = ginv[g];
         float v[4] = {s.x[m].x, s.x[m].y, s.x[m].z, s.x[m].w};
 #pragma unroll
@@ -377,8 +429,12 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
           v[3] += s.r[m].w;
         }
         s.x[m] = float4{v[0], v[1], v[2], v[3]};
-        if (in.mat != nullptr && q % a.blocks == wg)
-          *reinterpret_cast<float4*>(in.mat + b * in.mat_stride + 4 * q) = s.x[m];
+        if (in.mat != nullptr && r == wg) {
+          if constexpr (CHAIN)
+            st4_dev(in.mat + b * in.mat_stride + 4 * q, s.x[m]);
+          else
+            *reinterpret_cast<float4*>(in.mat + b * in.mat_stride + 4 * q) = s.x[m];
+        }
       }
     }
   }
@@ -390,16 +446,25 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
   lds_barrier();
 }
 
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool BF16, int NC>
-__device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean, float* ginv,
-                                          float* red) {
+// The wait of a stand-alone launch: the stream order has already made the input visible.
+struct NoWait {
+  __device__ bool operator()() const { return true; }
+};
+
+// One fused convolution by workgroup `wg` (of a.blocks) for sample `b`.  In CHAIN mode (a step of
+// the persistent tick kernel) it starts with `wait()` (a workgroup-uniform call that returns once
+// the producers of the input have finished, false if the launch is being abandoned), and the
+// input and all outputs use device-coherent accesses.
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool BF16, int NC,
+          bool CHAIN = false, typename Wait = NoWait>
+__device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* xs, float* gmean,
+                                          float* ginv, float* red, const Wait& wait = Wait{},
+                                          Override ov = Override{}) {
   constexpr int LOUT = lout_of(MODE, LIN);
   constexpr int TAPS = K + (RES ? 1 : 0);
   constexpr int NCH = NC;  // chunk slots per lane: the plan's chunk count, or the budget
   constexpr int V = RES ? 2 * LOUT : LOUT;
   const int tid = threadIdx.x;
-  const int wg = blockIdx.x;
-  const int b = blockIdx.y;
   const int rpt = kThreads / a.tpr;  // rows per tile
   const int gid = tid / a.tpr;
   const int lg = tid - gid * a.tpr;
@@ -409,13 +474,24 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
   const __amdgpu_buffer_rsrc_t wr = buffer_of(a.w, a.wbytes);
   const __amdgpu_buffer_rsrc_t rr = buffer_of(RES ? a.rw : a.w, RES ? a.rwbytes : a.wbytes);
   StageRegs<LIN, PRO> st;
+  if constexpr (CHAIN) {
+    // The input is produced by other workgroups of this launch: wait for them first (a wait
+    // issued behind weight loads would only complete once those arrive).  The parameters do not
+    // depend on them and are requested before.
+    if constexpr (VEC == 4) stage_params<LIN, PRO>(a, b, st, ov);
+    if (!wait()) return false;
+  }
   if constexpr (VEC == 4) {
-    stage_issue<LIN, PRO>(a, b, st);
+    stage_issue<LIN, PRO, CHAIN>(a, b, st, ov);
     // Every wavefront's prologue reads are issued before any wavefront's weight loads: a CU's
     // vector memory path returns data in order, so an input read queued behind weight misses
     // would only arrive with them.
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
+    // In the tick kernel every CU reaches this point at the same moment, so the CUs' first
+    // weight requests (tens of MB) would reach the memory channels together with the input
+    // reads and delay them by their whole transfer: the input is waited for first.
+    if constexpr (CHAIN) wait_vmem();
   }
   __builtin_amdgcn_sched_barrier(0);
   // The first tile's weights: EARLY chunks go out before the prologue (enough to keep HBM busy
@@ -430,7 +506,7 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
     load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (VEC == 4) stage_finish<LIN, PRO>(a, b, wg, st, xs, gmean, ginv);
+  if constexpr (VEC == 4) stage_finish<LIN, PRO, CHAIN>(a, b, wg, st, xs, gmean, ginv, ov);
 #pragma unroll
   for (int j = EARLY; j < NCH; ++j) {
     const int cv = lg + j * a.tpr;
@@ -439,7 +515,7 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
 
   const int waves = a.tpr / kWave;
   const int wig = lg / kWave;
-  const float* xsrc = a.in.src + b * a.in.src_stride;
+  const float* xsrc = (ov.src != nullptr ? ov.src : a.in.src) + b * a.in.src_stride;
   int parity = 0;
   // One row tile; `refill` (true for every tile but the workgroup's last) streams the next tile's
   // weights into each chunk's registers once its products are accumulated.  The last tile is a
@@ -485,7 +561,7 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
                                : a.in.plain + b * a.in.plain_stride +
                                      static_cast<std::int64_t>(cv - a.in.split) * LIN;
 #pragma unroll
-          for (int t = 0; t < LIN; ++t) xr[0][t] = p[t];
+          for (int t = 0; t < LIN; ++t) xr[0][t] = CHAIN ? ld_dev(p + t) : p[t];
         }
 #pragma unroll
         for (int t = 0; t < LOUT; ++t)
@@ -513,13 +589,17 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
 
     rs_step<V, 32>(acc, lane);
     const int off = rs_offset<V>(lane);
+    auto put = [&](float* p, float v) {
+      if constexpr (CHAIN) st_dev(p, v);
+      else *p = v;
+    };
     if (waves == 1) {
       if (rs_writer<V>(lane) && row < a.oc) {
         if (!RES || off < LOUT)
-          a.y[b * a.ys + static_cast<std::int64_t>(row) * LOUT + off] = acc[0] + a.bias[row];
+          put(a.y + b * a.ys + static_cast<std::int64_t>(row) * LOUT + off, acc[0] + a.bias[row]);
         else
-          a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + off - LOUT] =
-              acc[0] + a.rbias[row];
+          put(a.yr + b * a.yrs + static_cast<std::int64_t>(row) * LOUT + off - LOUT,
+              acc[0] + a.rbias[row]);
       }
       return;
     }
@@ -533,13 +613,15 @@ __device__ __forceinline__ void conv_body(const Args& a, float* xs, float* gmean
       float sum = 0.0f;
       for (int wv = 0; wv < waves; ++wv) sum += gred[wv * V + lg];
       if (!RES || lg < LOUT)
-        a.y[b * a.ys + static_cast<std::int64_t>(row) * LOUT + lg] = sum + a.bias[row];
+        put(a.y + b * a.ys + static_cast<std::int64_t>(row) * LOUT + lg, sum + a.bias[row]);
       else
-        a.yr[b * a.yrs + static_cast<std::int64_t>(row) * LOUT + lg - LOUT] = sum + a.rbias[row];
+        put(a.yr + b * a.yrs + static_cast<std::int64_t>(row) * LOUT + lg - LOUT,
+            sum + a.rbias[row]);
     }
   };
   for (; tile + a.blocks < a.tiles; tile += a.blocks) do_tile(tile, std::true_type{});
   do_tile(tile, std::false_type{});
+  return true;
 }
 
 template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, int NC>
@@ -550,13 +632,14 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
   __shared__ float gmean[kMaxGroups], ginv[kMaxGroups];
   __shared__ float red[2 * (kThreads / kWave) * V];
   float* xs = reinterpret_cast<float*>(xs4);
+  const int wg = blockIdx.x, b = blockIdx.y;
   if constexpr (VEC == 4) {
     if (a.bf16)
-      conv_body<MODE, K, LIN, VEC, PRO, RES, true, NC>(a, xs, gmean, ginv, red);
+      conv_body<MODE, K, LIN, VEC, PRO, RES, true, NC>(a, wg, b, xs, gmean, ginv, red);
     else
-      conv_body<MODE, K, LIN, VEC, PRO, RES, false, NC>(a, xs, gmean, ginv, red);
+      conv_body<MODE, K, LIN, VEC, PRO, RES, false, NC>(a, wg, b, xs, gmean, ginv, red);
   } else {
-    conv_body<MODE, K, LIN, VEC, PRO, RES, false, NC>(a, xs, gmean, ginv, red);
+    conv_body<MODE, K, LIN, VEC, PRO, RES, false, NC>(a, wg, b, xs, gmean, ginv, red);
   }
 }
 
@@ -639,6 +722,17 @@ hipError_t by_lin(int lin, int pro, bool res, const Args& a, int batch, hipStrea
     default: break;
   }
   return hipErrorInvalidValue;
+}
+
+// Host: the plan and arguments conv_fused launches with (false when it has no kernel for them);
+// `vec` and `pro` receive the instance's vector width and prologue kind.
+bool fused_args(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y, View yr,
+                int batch, Args& a, int& vec, int& pro);
+
+// Chunk slots of the kernel instance a plan with `nch` chunks per lane runs on (launch()).
+constexpr int instance_nc(int k, int lin, bool res, int vec, int nch) {
+  const int b = chunk_budget(k, lin, res, vec);
+  return nch == 1 ? 1 : (nch == 2 && b > 2 ? 2 : (nch == 4 && b > 4 ? 4 : b));
 }
 
 // Launchers, one translation unit each (they instantiate the kernel for every length/prologue).

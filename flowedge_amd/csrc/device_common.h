@@ -19,17 +19,64 @@ __device__ __forceinline__ float mish_f(float v) {
 }
 
 // Same identity with the hardware exp2 (v_exp_f32) and reciprocal (v_rcp_f32), each about 1 ULP:
-// the prologue form, where every workgroup transforms a whole activation tensor.
+// the prologue form, where every workgroup transforms a whole activation tensor.  Branch-free
+// (the exponent is clamped and the large-v case selected), so a wavefront never splits on it.
 __device__ __forceinline__ float mish_fast(float v) {
-  if (v > 20.0f) return v;
-  const float e = __builtin_amdgcn_exp2f(v * 1.44269504088896341f);
+  const float e = __builtin_amdgcn_exp2f(fminf(v, 20.0f) * 1.44269504088896341f);
   const float n = e * (e + 2.0f);
-  return v * n * __builtin_amdgcn_rcpf(n + 2.0f);
+  const float m = v * n * __builtin_amdgcn_rcpf(n + 2.0f);
+  return v > 20.0f ? v : m;
 }
 
 __device__ __forceinline__ float bf16_to_f32(unsigned short bits) {
   return __uint_as_float(static_cast<unsigned>(bits) << 16);
 }
+
+// Device-coherent accesses for data that workgroups of one running kernel hand to each other
+// (the persistent tick kernel): relaxed agent-scope atomics, which gfx950 performs as loads and
+// stores with the sc1 (device scope) cache policy, read and write at the device's coherence
+// point, so no XCD's L2 or CU's L1 serves a stale copy and no whole-cache write-back or
+// invalidation is needed.
+// Global (address space 1) views of generic pointers, so the accesses compile to global_*
+// instructions rather than flat ones (which would also hold the LDS wait counter).
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(global_ptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(global_ptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_dev(const unsigned* p) {
+  return __hip_atomic_load(global_ptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(unsigned* p, unsigned v) {
+  __hip_atomic_store(global_ptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16-byte accesses as two 8-byte device-scope atomics (per-lane addresses, 8-byte aligned).
+__device__ __forceinline__ float4 ld4_dev(const float* p) {
+  const auto* q = global_ptr(reinterpret_cast<const unsigned long long*>(p));
+  const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return float4{__uint_as_float(static_cast<unsigned>(lo)),
+                __uint_as_float(static_cast<unsigned>(lo >> 32)),
+                __uint_as_float(static_cast<unsigned>(hi)),
+                __uint_as_float(static_cast<unsigned>(hi >> 32))};
+}
+__device__ __forceinline__ void st4_dev(float* p, float4 v) {
+  auto* q = global_ptr(reinterpret_cast<unsigned long long*>(p));
+  const unsigned long long lo = static_cast<unsigned long long>(__float_as_uint(v.x)) |
+                                (static_cast<unsigned long long>(__float_as_uint(v.y)) << 32);
+  const unsigned long long hi = static_cast<unsigned long long>(__float_as_uint(v.z)) |
+                                (static_cast<unsigned long long>(__float_as_uint(v.w)) << 32);
+  __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every earlier vector memory access of this wavefront has completed (stores
+// acknowledged by the device-coherent level).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // The value `v` of this lane's exchange partner for bit MASK, through VALU cross-lane moves: DPP
 // quad_perm (lane ^ 1, lane ^ 2), DPP row_ror 8 (lane ^ 8 within a 16-lane row) and the gfx950

@@ -206,6 +206,7 @@ struct GraphEntry {
   int kind = 0, mode = 0;
   std::size_t batch = 0, steps = 0;
   hipGraphExec_t exec = nullptr;
+  int chain_table = -1;  // persistent tick: index of its evaluation table, else -1
 };
 
 }  // namespace
@@ -264,6 +265,17 @@ struct FeEngine {
 
   std::list<GraphEntry> graphs;  // most recently used first
   std::uint64_t captures = 0;    // graphs captured and instantiated so far
+
+  // Persistent batch-1 tick (chain.hip): one launch runs every evaluation of a tick.
+  bool chain_on = false;          // B=1 sampling ticks use the tick kernel
+  std::string chain_why = "not built";  // why they do not
+  int chain_nsteps = 0;
+  std::size_t chain_steps = 0;    // step table [kMaxChainSteps]
+  std::size_t chain_flags = 0, chain_abort = 0, chain_slots = 0;
+  std::size_t chain_tables = 0;   // kChainTables evaluation tables of kMaxChainEvals entries
+  int chain_slot_floats = 0;
+  std::uint64_t chain_abandoned = 0;  // ticks the kernel gave up on (re-run on per-layer graphs)
+  unsigned* pin_status = nullptr;     // the tick's abort flag, copied back after each tick
 
   // Model identity (engine_runtime.cc:159-161).
   std::array<std::uint8_t, 16> digest{};
@@ -334,6 +346,10 @@ static_assert(sizeof(fe_action_metadata) == 80);
 namespace {
 
 constexpr std::size_t kGraphCache = 32;
+// Persistent ticks: one evaluation table per cached graph, of at most this many evaluations
+// (longer solves run on per-layer graphs).
+constexpr std::size_t kChainTables = kGraphCache;
+constexpr std::size_t kMaxChainEvals = 128;
 
 void end_solve(FeEngine* e);
 
@@ -485,6 +501,18 @@ struct Builder {
     if (c.prediction == 0) e.ddim_table = plan.take(c.train_timesteps * F * 4);
     // U-Net evaluations per call: diffusion <= T steps, flow RK4 4 per step.
     e.max_nfe = std::max<std::size_t>(c.train_timesteps, 1024);
+    // Persistent tick: step table, per-workgroup counters and state slots (x, xin and four flow
+    // stages), evaluation tables.
+    const std::size_t v = c.horizon * c.action_dim;
+    if (fe::hip::chain_supported_horizon(static_cast<int>(c.horizon)) && c.action_dim <= 64) {
+      e.chain_steps = plan.take(fe::hip::kMaxChainSteps * fe::hip::chain_step_bytes());
+      e.chain_flags = plan.take(fe::hip::kChainGrid * fe::hip::kChainFlagStride * 4);
+      e.chain_abort = plan.take(4);
+      e.chain_slot_floats = static_cast<int>((6 * v + 63) / 64 * 64);
+      e.chain_slots = plan.take(static_cast<std::size_t>(fe::hip::kChainGrid) *
+                                e.chain_slot_floats * 4);
+      e.chain_tables = plan.take(kChainTables * kMaxChainEvals * sizeof(fe::hip::ChainEval));
+    }
     return true;
   }
 };
@@ -897,6 +925,20 @@ hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, c
   return hipSuccess;
 }
 
+// Fields of the final GroupNorm + Mish + 1x1 conv that every update of the engine shares.
+void update_base(const FeEngine& e, fe::hip::UpdateOp& upd) {
+  const Config& c = e.cfg;
+  upd.c0 = static_cast<int>(c.dims[0]);
+  upd.horizon = static_cast<int>(c.horizon);
+  upd.action_dim = static_cast<int>(c.action_dim);
+  upd.h = e.wp(e.w.fconv_out);
+  upd.gamma = e.ptr(e.fnorm.g_off);
+  upd.beta = e.ptr(e.fnorm.b_off);
+  upd.groups = static_cast<int>(kFinalNormGroups);
+  upd.wo = static_cast<const float*>(e.fout.op.w);
+  upd.bo = e.fout.op.b;
+}
+
 // One U-Net evaluation on xin (FiLM time row `film_row`), ending with `upd`
 // (diffusion.cc:793-914).
 hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::UpdateOp upd) {
@@ -1022,15 +1064,7 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
   fi.src_stride = fs;
   fi.split = static_cast<int>(c.dims[0]);
   FE_TRY(conv(e, "final.conv", e.fconv.op, nullptr, fi, View{fo, fs}, View{}, batch, s));
-  upd.c0 = static_cast<int>(c.dims[0]);
-  upd.horizon = static_cast<int>(c.horizon);
-  upd.action_dim = static_cast<int>(c.action_dim);
-  upd.h = fo;
-  upd.gamma = e.ptr(e.fnorm.g_off);
-  upd.beta = e.ptr(e.fnorm.b_off);
-  upd.groups = static_cast<int>(kFinalNormGroups);
-  upd.wo = static_cast<const float*>(e.fout.op.w);
-  upd.bo = e.fout.op.b;
+  update_base(e, upd);
   if (e.dry) return hipSuccess;
   return update(upd, batch, s);
 }
@@ -1079,8 +1113,10 @@ hipError_t enqueue_diffusion_start(FeEngine& e, int batch) {
   return enqueue_film_cond(e, batch);
 }
 
-hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int scheduler,
-                                  const float* alphas, std::size_t i) {
+// The update after step i of a DDIM/DDPM solve of `steps` steps and the timestep that step
+// evaluates (diffusion.cc:928-1024); the scalars are computed on the host as the reference does.
+fe::hip::UpdateOp diffusion_update(FeEngine& e, std::size_t steps, int scheduler,
+                                   const float* alphas, std::size_t i, std::size_t& t_out) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   const std::size_t ratio = c.train_timesteps / steps;
@@ -1113,6 +1149,14 @@ hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int
     u.add_noise = prev >= 0 ? 1 : 0;
     u.noise_offset = static_cast<std::uint64_t>(i) * e.values;
   }
+  t_out = t;
+  return u;
+}
+
+hipError_t enqueue_diffusion_step(FeEngine& e, int batch, std::size_t steps, int scheduler,
+                                  const float* alphas, std::size_t i) {
+  std::size_t t = 0;
+  const fe::hip::UpdateOp u = diffusion_update(e, steps, scheduler, alphas, i, t);
   const float* row = e.ptr(e.ddim_table) + t * e.film_total;
   return enqueue_unet(e, batch, row, u);
 }
@@ -1150,13 +1194,13 @@ hipError_t enqueue_flow_start(FeEngine& e, int batch, std::size_t steps, int met
   return enqueue_film(e, ts, static_cast<int>(steps * flow_stages(method)), batch);
 }
 
-hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int method,
-                             std::size_t step) {
+// The update after stage j of a flow step (flow.cc:291-318, span_ops.h:27-52).
+fe::hip::UpdateOp flow_update(FeEngine& e, std::size_t steps, int method, int j) {
   using namespace fe::hip;
   const int stages = static_cast<int>(flow_stages(method));
   const float dt = 1.0f / static_cast<float>(steps);
   const float half_dt = 0.5f * dt;
-  for (int j = 0; j < stages; ++j) {
+  {
     UpdateOp u{};
     u.x = e.wp(e.w.x_state);
     u.xin = e.wp(e.w.x_in);
@@ -1181,6 +1225,15 @@ hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int meth
         u.kind = kUpdateRK4;
       }
     }
+    return u;
+  }
+}
+
+hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int method,
+                             std::size_t step) {
+  const int stages = static_cast<int>(flow_stages(method));
+  for (int j = 0; j < stages; ++j) {
+    const fe::hip::UpdateOp u = flow_update(e, steps, method, j);
     const std::size_t n = step * static_cast<std::size_t>(stages) + static_cast<std::size_t>(j);
     FE_TRY(enqueue_unet(e, batch, e.wp(e.w.film_table) + n * e.film_total, u));
   }
@@ -1238,19 +1291,111 @@ hipError_t capture_graph(FeEngine& e, Body&& body, hipGraphExec_t& exec) {
   return st;
 }
 
-// Returns the cached graph for this shape, capturing it on first use.
+// U-Net evaluations of a sampling call.
+std::size_t evaluations(int kind, std::size_t steps, int mode) {
+  return kind == 0 ? steps : steps * flow_stages(mode);
+}
+
+// Fills evaluation table `table` of the persistent tick for this solve: each evaluation's FiLM
+// time rows and the update after it, computed exactly as the per-layer graphs compute them.
+hipError_t fill_chain_table(FeEngine& e, int kind, std::size_t steps, int mode, int table) {
+  using namespace fe::hip;
+  const Config& c = e.cfg;
+  std::vector<ChainEval> evals;
+  if (kind == 0) {
+    const std::vector<float> alphas = alphas_cumprod(c.train_timesteps);
+    for (std::size_t i = 0; i < steps; ++i) {
+      std::size_t t = 0;
+      ChainEval ev;
+      ev.upd = diffusion_update(e, steps, mode, alphas.data(), i, t);
+      update_base(e, ev.upd);
+      ev.film_row = e.ptr(e.ddim_table) + t * e.film_total;
+      evals.push_back(ev);
+    }
+  } else {
+    const int stages = static_cast<int>(flow_stages(mode));
+    for (std::size_t st = 0; st < steps; ++st)
+      for (int j = 0; j < stages; ++j) {
+        ChainEval ev;
+        ev.upd = flow_update(e, steps, mode, j);
+        update_base(e, ev.upd);
+        ev.film_row = e.wp(e.w.film_table) + (st * stages + j) * e.film_total;
+        evals.push_back(ev);
+      }
+  }
+  ChainEval* dst = e.ptr<ChainEval>(e.chain_tables) + static_cast<std::size_t>(table) * kMaxChainEvals;
+  return hipMemcpy(dst, evals.data(), evals.size() * sizeof(ChainEval), hipMemcpyHostToDevice);
+}
+
+// One batch-1 tick on the persistent kernel: the solve's start (noise into the state, FiLM rows),
+// the tick kernel, the readout, and a copy of the tick's abort flag to the host.
+hipError_t enqueue_chain_tick(FeEngine& e, int kind, std::size_t steps, int mode, int table) {
+  using namespace fe::hip;
+  FE_TRY(kind == 0 ? enqueue_diffusion_start(e, 1) : enqueue_flow_start(e, 1, steps, mode));
+  ChainTick t;
+  t.steps = e.ptr<char>(e.chain_steps);
+  t.nsteps = e.chain_nsteps;
+  t.evals = e.ptr<ChainEval>(e.chain_tables) + static_cast<std::size_t>(table) * kMaxChainEvals;
+  t.nevals = static_cast<int>(evaluations(kind, steps, mode));
+  t.x0 = e.wp(e.w.x_state);
+  t.xin0 = e.wp(e.w.x_in);
+  t.slots = e.ptr(e.chain_slots);
+  t.slot_floats = e.chain_slot_floats;
+  t.x_out = e.wp(e.w.x_state);
+  t.flags = e.ptr<unsigned>(e.chain_flags);
+  t.abort = e.ptr<unsigned>(e.chain_abort);
+  t.spin_limit = 1ll << 22;
+  t.values = static_cast<int>(e.values);
+  t.horizon = static_cast<int>(e.cfg.horizon);
+  FE_TRY(chain_tick(t, e.stream));
+  FE_TRY(kind == 0 ? enqueue_diffusion_readout(e, 1) : enqueue_flow_readout(e, 1));
+  return hipMemcpyAsync(e.pin_status, e.ptr(e.chain_abort), 4, hipMemcpyDeviceToHost, e.stream);
+}
+
+// Drops the cached persistent-tick graphs (after a tick was abandoned).
+void drop_chain_graphs(FeEngine& e) {
+  for (auto it = e.graphs.begin(); it != e.graphs.end();) {
+    if (it->chain_table >= 0) {
+      (void)hipGraphExecDestroy(it->exec);
+      it = e.graphs.erase(it);
+    } else {
+      ++it;
+    }
+  }
+}
+
+// Returns the cached graph for this shape, capturing it on first use.  Batch-1 solves of up to
+// kMaxChainEvals evaluations run as one persistent tick when the engine has a step table.
 hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps, int mode,
-                     hipGraphExec_t& exec) {
+                     hipGraphExec_t& exec, bool* chained = nullptr) {
+  const bool chain =
+      e.chain_on && batch == 1 && evaluations(kind, steps, mode) <= kMaxChainEvals;
+  if (chained != nullptr) *chained = chain;
   for (auto it = e.graphs.begin(); it != e.graphs.end(); ++it)
-    if (it->kind == kind && it->batch == batch && it->steps == steps && it->mode == mode) {
+    if (it->kind == kind && it->batch == batch && it->steps == steps && it->mode == mode &&
+        (it->chain_table >= 0) == chain) {
       e.graphs.splice(e.graphs.begin(), e.graphs, it);
       exec = it->exec;
       return hipSuccess;
     }
+  if (e.graphs.size() >= kGraphCache) {
+    (void)hipGraphExecDestroy(e.graphs.back().exec);
+    e.graphs.pop_back();
+  }
+  int table = -1;
+  if (chain) {
+    std::vector<bool> used(kChainTables, false);
+    for (const GraphEntry& g : e.graphs)
+      if (g.chain_table >= 0) used[static_cast<std::size_t>(g.chain_table)] = true;
+    for (std::size_t i = 0; i < kChainTables && table < 0; ++i)
+      if (!used[i]) table = static_cast<int>(i);
+    FE_TRY(fill_chain_table(e, kind, steps, mode, table));
+  }
   hipGraphExec_t inst = nullptr;
   FE_TRY(capture_graph(
       e,
       [&]() {
+        if (chain) return enqueue_chain_tick(e, kind, steps, mode, table);
         if (kind == 0) {
           const std::vector<float> alphas = alphas_cumprod(e.cfg.train_timesteps);
           return enqueue_diffusion(e, static_cast<int>(batch), steps, mode, alphas.data());
@@ -1258,11 +1403,7 @@ hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps
         return enqueue_flow(e, static_cast<int>(batch), steps, mode);
       },
       inst));
-  if (e.graphs.size() >= kGraphCache) {
-    (void)hipGraphExecDestroy(e.graphs.back().exec);
-    e.graphs.pop_back();
-  }
-  e.graphs.push_front(GraphEntry{kind, mode, batch, steps, inst});
+  e.graphs.push_front(GraphEntry{kind, mode, batch, steps, inst, table});
   exec = inst;
   return hipSuccess;
 }
@@ -1330,10 +1471,12 @@ int check_sample(const FeEngine* e, int kind, std::size_t batch, std::size_t ste
   return FE_STATUS_OK;
 }
 
-// Replays the sampling graph; inputs already in the engine's device input buffers.
-int run_graph(FeEngine* e, int kind, std::size_t batch, std::size_t steps, int mode) {
+// Replays the sampling graph; inputs already in the engine's device input buffers.  `chained`
+// tells whether it was a persistent tick (whose abort flag the caller checks after the sync).
+int run_graph(FeEngine* e, int kind, std::size_t batch, std::size_t steps, int mode,
+              bool& chained) {
   hipGraphExec_t exec = nullptr;
-  hipError_t st = get_graph(*e, kind, batch, steps, mode, exec);
+  hipError_t st = get_graph(*e, kind, batch, steps, mode, exec, &chained);
   if (st != hipSuccess) return hip_fail("Failed to build sampling graph", st);
   if ((st = hipEventRecord(e->ev0, e->stream)) != hipSuccess ||
       (st = hipGraphLaunch(exec, e->stream)) != hipSuccess ||
@@ -1341,6 +1484,18 @@ int run_graph(FeEngine* e, int kind, std::size_t batch, std::size_t steps, int m
     return hip_fail("Sampling graph launch failed", st);
   e->timed = true;
   return FE_STATUS_OK;
+}
+
+// After a synchronised persistent tick: true when the kernel abandoned it (a workgroup never
+// started, e.g. other work held CUs).  The engine then stops using the tick kernel and the caller
+// runs the call again on the per-layer graphs (its inputs are still in the device buffers).
+bool chain_abandoned(FeEngine* e, bool chained) {
+  if (!chained || *e->pin_status == 0) return false;
+  e->chain_on = false;
+  e->chain_why = "a persistent tick was abandoned (not every workgroup was resident)";
+  ++e->chain_abandoned;
+  drop_chain_graphs(*e);
+  return true;
 }
 
 int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, std::size_t batch,
@@ -1362,12 +1517,16 @@ int sample_host(FeEngine* e, int kind, const float* cond, const float* noise, st
       (st = hipMemcpyAsync(e->wp(e->w.seed), e->pin_seed, 8, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess)
     return hip_fail("Input upload failed", st);
-  const int r = run_graph(e, kind, batch, steps, mode);
-  if (r != FE_STATUS_OK) return r;
-  if ((st = hipMemcpyAsync(e->pin_action, e->wp(e->w.out_action), nv * 4, hipMemcpyDeviceToHost,
-                           e->stream)) != hipSuccess ||
-      (st = hipStreamSynchronize(e->stream)) != hipSuccess)
-    return hip_fail("Sampling failed", st);
+  bool chained = false;
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    const int r = run_graph(e, kind, batch, steps, mode, chained);
+    if (r != FE_STATUS_OK) return r;
+    if ((st = hipMemcpyAsync(e->pin_action, e->wp(e->w.out_action), nv * 4,
+                             hipMemcpyDeviceToHost, e->stream)) != hipSuccess ||
+        (st = hipStreamSynchronize(e->stream)) != hipSuccess)
+      return hip_fail("Sampling failed", st);
+    if (!chain_abandoned(e, chained)) break;
+  }
   std::memcpy(action, e->pin_action, nv * 4);
   return FE_STATUS_OK;
 }
@@ -1554,6 +1713,76 @@ std::size_t env_max_batch() {
   return (end && *end == '\0' && n > 0 && n <= 65535) ? n : 0;
 }
 
+// Builds the persistent tick's step table from the U-Net's convolutions at batch 1 (the listing
+// the diagnostics use); leaves chain_on false, with the reason, when the tick kernel cannot run
+// this model or this device.
+void build_chain(FeEngine& e) {
+  using namespace fe::hip;
+  // Opt-in: on MI355X the per-layer graphs are as fast (pusht DDIM-10 B=1: 3.465 against
+  // 3.485 ms device p50), so they stay the default.
+  const char* v = std::getenv("FLOWEDGE_PERSISTENT");
+  if (v == nullptr || std::strcmp(v, "1") != 0) {
+    e.chain_why = "not requested (FLOWEDGE_PERSISTENT=1 at load selects it)";
+    return;
+  }
+  if (e.chain_steps == 0) {
+    e.chain_why = "horizon or action count outside the tick kernel's instances";
+    return;
+  }
+  if (e.mfma_batch <= 1) {
+    e.chain_why = "batch 1 runs on the matrix cores (FLOWEDGE_MFMA_BATCH)";
+    return;
+  }
+  if (e.cfg.dims[0] > 1024) {  // the update's per-workgroup channel capacity (update_body.h)
+    e.chain_why = "final width above 1024";
+    return;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e.device) != hipSuccess ||
+      cus < kChainGrid) {
+    e.chain_why = "fewer compute units than the tick kernel's workgroups";
+    return;
+  }
+  if (ensure_conv_records(&e) != FE_STATUS_OK) {
+    e.chain_why = "convolution listing failed";
+    clear_error();
+    return;
+  }
+  std::vector<ChainConv> convs;
+  for (std::size_t i = 0; i < e.conv_records.size(); ++i) {
+    const FeEngine::ConvRecord& r = e.conv_records[i];
+    ChainConv c;
+    c.op = r.op;
+    c.has_res = r.has_res;
+    c.res = r.res;
+    c.in = r.in;
+    c.y = r.y;
+    c.yr = r.yr;
+    c.film = r.in.film_time != nullptr;
+    c.state = i == 0;
+    if (c.state && r.in.src != e.wp(e.w.x_in)) {
+      e.chain_why = "first convolution does not read the U-Net input";
+      return;
+    }
+    convs.push_back(c);
+  }
+  const int n = static_cast<int>(convs.size());
+  std::vector<char> host(static_cast<std::size_t>(n) * chain_step_bytes());
+  const char* why = "";
+  if (!chain_build(convs.data(), n, host.data(), &why)) {
+    e.chain_why = why;
+    return;
+  }
+  if (hipMemcpy(e.ptr<char>(e.chain_steps), host.data(), host.size(), hipMemcpyHostToDevice) !=
+      hipSuccess) {
+    e.chain_why = "step table upload failed";
+    return;
+  }
+  e.chain_nsteps = n;
+  e.chain_on = true;
+  e.chain_why = "";
+}
+
 fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned threads) {
   if (threads > kMaxPoolThreads) {
     set_error("Worker thread count must be from 0 through 8");
@@ -1647,6 +1876,8 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   e->pin_action = e->pin_noise + nv;
   e->pin_seed = reinterpret_cast<std::uint64_t*>(
       (reinterpret_cast<std::uintptr_t>(e->pin_action + nv) + 15) & ~std::uintptr_t{15});
+  e->pin_status = reinterpret_cast<unsigned*>(e->pin_seed + 1);
+  *e->pin_status = 0;
   if ((st = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
       (st = hipEventCreate(&e->ev0)) != hipSuccess || (st = hipEventCreate(&e->ev1)) != hipSuccess) {
     hip_fail("Stream creation failed", st);
@@ -1668,6 +1899,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
       return nullptr;
     }
   }
+  build_chain(*e);
   return e.release();
 }
 
@@ -2026,12 +2258,16 @@ int fe_engine_sample_device(fe_engine* engine, int kind, const float* condition_
       (st = hipMemcpyAsync(e->wp(e->w.seed), e->pin_seed, 8, hipMemcpyHostToDevice,
                            e->stream)) != hipSuccess)
     return hip_fail("Input copy failed", st);
-  const int r = run_graph(e, kind, batch, steps, mode);
-  if (r != FE_STATUS_OK) return r;
-  if ((st = hipMemcpyAsync(action_dev, e->wp(e->w.out_action), nv * 4, hipMemcpyDeviceToDevice,
-                           e->stream)) != hipSuccess ||
-      (st = hipStreamSynchronize(e->stream)) != hipSuccess)
-    return hip_fail("Sampling failed", st);
+  bool chained = false;
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    const int r = run_graph(e, kind, batch, steps, mode, chained);
+    if (r != FE_STATUS_OK) return r;
+    if ((st = hipMemcpyAsync(action_dev, e->wp(e->w.out_action), nv * 4,
+                             hipMemcpyDeviceToDevice, e->stream)) != hipSuccess ||
+        (st = hipStreamSynchronize(e->stream)) != hipSuccess)
+      return hip_fail("Sampling failed", st);
+    if (!chain_abandoned(e, chained)) break;
+  }
   return FE_STATUS_OK;
 }
 
@@ -2246,6 +2482,14 @@ uint64_t fe_device_alloc_count(void) { return g_device_allocs.load(); }
 
 uint64_t fe_engine_graph_captures(const fe_engine* engine) {
   return engine != nullptr ? engine->captures : 0;
+}
+
+int fe_engine_persistent_tick(const fe_engine* engine) {
+  return engine != nullptr && engine->chain_on ? 1 : 0;
+}
+
+const char* fe_engine_persistent_tick_reason(const fe_engine* engine) {
+  return engine != nullptr ? engine->chain_why.c_str() : "no engine";
 }
 
 int fe_engine_conv_count(fe_engine* engine, size_t* count) {

@@ -185,6 +185,56 @@ hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
 hipError_t finish_sample(const float* x, const float* amin, const float* amax, float* action,
                          int batch, int horizon, int action_dim, hipStream_t stream);
 
+// ---- Persistent tick (chain.hip) ----
+// One sampling tick of one sample in a single launch: kChainGrid workgroups (one per CU) run every
+// convolution of every U-Net evaluation as the steps of one step table, handing activations to
+// each other through device-coherent memory and per-workgroup completion counters (a step's
+// workgroups request their first weights, then wait until every workgroup has finished the
+// previous step).  Each workgroup computes every evaluation's sampler update itself and keeps the
+// sample's state in a slot of its own, so updates need no hand-off.
+constexpr int kChainGrid = 256;
+constexpr int kChainFlagStride = 64;  // unsigned per workgroup counter (256 bytes apart)
+constexpr int kMaxChainSteps = 64;
+
+// One convolution of an evaluation (enqueue order).
+struct ChainConv {
+  ConvOp op;
+  bool has_res = false;
+  ConvOp res;
+  ConvInput in;
+  View y, yr;
+  bool film = false;   // its FiLM time rows are those of the evaluation being run
+  bool state = false;  // its input is the workgroup's U-Net input slot (first convolution)
+};
+struct ChainEval {
+  const float* film_row = nullptr;  // FiLM time rows of this evaluation
+  UpdateOp upd;                     // sampler update after it (x, xin, kbuf: the slot's)
+};
+struct ChainTick {
+  const void* steps = nullptr;
+  int nsteps = 0;
+  const ChainEval* evals = nullptr;
+  int nevals = 0;
+  const float* x0 = nullptr;   // state [A][H] at the start
+  const float* xin0 = nullptr; // first U-Net input [A][H]
+  float* slots = nullptr;      // per workgroup: x, xin, k0 .. k3, `values` floats each
+  int slot_floats = 0;
+  float* x_out = nullptr;      // final state, written by workgroup 0
+  unsigned* flags = nullptr;   // [kChainGrid * kChainFlagStride]
+  unsigned* abort = nullptr;   // set when a wait gives up (the tick's result is then invalid)
+  long long spin_limit = 0;    // polls before a wait gives up
+  int values = 0;              // A * H
+  int horizon = 0;
+};
+std::size_t chain_step_bytes();
+// Horizons the tick kernel is built for.
+bool chain_supported_horizon(int horizon);
+// Step table of one evaluation (host memory of n * chain_step_bytes()); false, with the reason,
+// when a convolution has no variant in the tick kernel.
+bool chain_build(const ChainConv* convs, int n, void* steps, const char** why);
+// Enqueues the counter reset and the tick kernel.
+hipError_t chain_tick(const ChainTick& t, hipStream_t stream);
+
 // Static device scratch of the allocation-free entry point (scratch.hip): kScratchBytes per GPU.
 // scratch_setup returns the array's device address on `device`, which must be the current device;
 // the address is looked up once per device and kept.

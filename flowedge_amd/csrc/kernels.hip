@@ -11,6 +11,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "update_body.h"
 
 namespace fe::hip {
 namespace {
@@ -155,226 +156,11 @@ __global__ void begin_kernel(const float* noise, float* x, float* xin, int h, in
   }
 }
 
-// splitmix64 (diffusion.cc:214-221): call i of the stream seeded `seed` mixes seed + (i+2)*GAMMA.
-__device__ __forceinline__ float stream_uniform(std::uint64_t seed, std::uint64_t call) {
-  std::uint64_t z = seed + (call + 2ull) * 0x9e3779b97f4a7c15ULL;
-  z = (z ^ (z >> 30u)) * 0xbf58476d1ce4e5b9ULL;
-  z = (z ^ (z >> 27u)) * 0x94d049bb133111ebULL;
-  z ^= z >> 31u;
-  return static_cast<float>((z >> 40u) + 1u) / 16777217.0f;
-}
-
-// Value `n` of the reference's Box-Muller stream (pairs: cos first, then sin).
-__device__ __forceinline__ float stream_gaussian(std::uint64_t seed, std::uint64_t n) {
-  const std::uint64_t pair = n >> 1;
-  const float first = fmaxf(stream_uniform(seed, 2 * pair), 1.17549435e-38f);
-  const float second = stream_uniform(seed, 2 * pair + 1);
-  const float radius = sqrtf(-2.0f * logf(first));
-  const float angle = 6.28318530717958647692f * second;
-  return (n & 1) ? radius * sinf(angle) : radius * cosf(angle);
-}
-
-// The sampler update of state value (a, t) (state layout [A][H]) from the U-Net output e and
-// the current state xv (diffusion.cc:995-1024, flow.cc:291-318).
-__device__ __forceinline__ void apply_update(const UpdateOp& op, std::int64_t sample, int a, int t,
-                                             int A, int H, float e, float xv) {
-  const std::int64_t si = sample + static_cast<std::int64_t>(a) * H + t;
-  switch (op.kind) {
-    case kUpdateDenoise:
-      op.out[sample + static_cast<std::int64_t>(t) * A + a] = e;
-      break;
-    case kUpdateDDIM: {
-      float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
-      if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
-      const float nx = op.sqrt_ap * x0 + op.sqrt_1map * e;
-      op.x[si] = nx;
-      if (op.xin != op.x) op.xin[si] = nx;
-      break;
-    }
-    case kUpdateDDPM: {
-      float x0 = (xv - op.sqrt_bt * e) / op.sqrt_at;
-      if (op.clip) x0 = fminf(fmaxf(x0, -op.clip_range), op.clip_range);
-      float nx = op.coef_x0 * x0 + op.coef_x * xv;
-      if (op.add_noise)
-        nx += op.sigma *
-              stream_gaussian(*op.seed, op.noise_offset + static_cast<std::uint64_t>(t) * A + a);
-      op.x[si] = nx;
-      if (op.xin != op.x) op.xin[si] = nx;
-      break;
-    }
-    case kUpdateEuler: {
-      const float nx = xv + op.dt * e;
-      op.x[si] = nx;
-      op.xin[si] = nx;
-      break;
-    }
-    case kUpdateStage: {
-      const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
-      op.kbuf[op.slot * plane + si] = e;
-      op.xin[si] = xv + op.dt * e;
-      break;
-    }
-    case kUpdateHeun: {
-      const float k1 = op.kbuf[si];
-      const float nx = xv + 0.5f * op.dt * (k1 + e);
-      op.x[si] = nx;
-      op.xin[si] = nx;
-      break;
-    }
-    case kUpdateRK4: {
-      const std::int64_t plane = static_cast<std::int64_t>(gridDim.x) * A * H;
-      const float k1 = op.kbuf[si], k2 = op.kbuf[plane + si], k3 = op.kbuf[2 * plane + si];
-      const float nx = xv + (op.dt / 6.0f) * (k1 + 2.0f * k2 + 2.0f * k3 + e);
-      op.x[si] = nx;
-      op.xin[si] = nx;
-      break;
-    }
-    default:
-      break;
-  }
-}
-
-constexpr int kUpdThreads = 512;
-constexpr int kMaxUpdateChannelsPerLane = 2;  // c0 <= 1024
-constexpr int kMaxUpdateGroups = 32;
-constexpr int kMaxActions = 64;
-
-// One block per sample.  Lane l owns channels l and l + 512 (H positions each, loaded as 16-byte
-// vectors); the block reduces the GroupNorm statistics (fp64), applies GN + Mish, and forms the
-// 1x1 conv's partial sums for up to 64 / H actions at a time, folded by one wavefront
-// reduce-scatter and one LDS pass per action group.  The update then runs on the A*H state values.
+// Final GroupNorm + Mish + 1x1 conv + sampler update, one workgroup per sample (update_body.h).
 template <int H>
-__global__ __launch_bounds__(kUpdThreads) void update_kernel(UpdateOp op) {
-  constexpr int CPL = kMaxUpdateChannelsPerLane;
-  constexpr int AG = H >= kWave ? 1 : kWave / H;  // actions per reduction pass
-  constexpr int V = AG * H;
-  __shared__ double ps[kUpdThreads * CPL];
-  __shared__ double pq[kUpdThreads * CPL];
-  __shared__ float gmean[kMaxUpdateGroups], ginv[kMaxUpdateGroups];
-  __shared__ float red[kUpdThreads / kWave][V];
-  __shared__ float eps[kMaxActions][H];
-  const int b = blockIdx.x;
-  const int A = op.action_dim, C = op.c0;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
-  const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
-  const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
-
-  // Reads that do not depend on the statistics are issued first, so their latency overlaps the
-  // reduction: the output conv's weights for the first action group and the sampler state.
-  constexpr int XPL = (kMaxActions * H + kUpdThreads - 1) / kUpdThreads;  // state values per lane
-  float w0[AG][CPL];
-#pragma unroll
-  for (int aa = 0; aa < AG; ++aa)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = tid + i * kUpdThreads;
-      w0[aa][i] = c < C && aa < A ? op.wo[static_cast<std::int64_t>(aa) * C + c] : 0.0f;
-    }
-  float xs[XPL];
-#pragma unroll
-  for (int r = 0; r < XPL; ++r) {
-    const int i = tid + r * kUpdThreads;
-    xs[r] = op.kind != kUpdateDenoise && i < A * H ? op.x[sample + i] : 0.0f;
-  }
-
-  float hv[CPL][H];
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = tid + i * kUpdThreads;
-    const float* p = hb + static_cast<std::int64_t>(c) * H;
-    if constexpr (H >= 4) {
-#pragma unroll
-      for (int t = 0; t < H; t += 4) {
-        const float4 v = c < C ? *reinterpret_cast<const float4*>(p + t) : float4{0, 0, 0, 0};
-        hv[i][t] = v.x;
-        hv[i][t + 1] = v.y;
-        hv[i][t + 2] = v.z;
-        hv[i][t + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < H; ++t) hv[i][t] = c < C ? p[t] : 0.0f;
-    }
-    double s = 0.0, q = 0.0;
-#pragma unroll
-    for (int t = 0; t < H; ++t) {
-      const double d = static_cast<double>(hv[i][t]);
-      s += d;
-      q += d * d;
-    }
-    if (c < C) {
-      ps[c] = s;
-      pq[c] = q;
-    }
-  }
-  __syncthreads();
-  const int cpg = C / op.groups;
-  for (int g = wave; g < op.groups; g += kUpdThreads / kWave) {
-    double s = 0.0, q = 0.0;
-    for (int i = lane; i < cpg; i += kWave) {
-      s += ps[g * cpg + i];
-      q += pq[g * cpg + i];
-    }
-    s = wave_sum(s);
-    q = wave_sum(q);
-    if (lane == 0) {
-      const double n = static_cast<double>(cpg) * H;
-      const double mean = s / n;
-      const double var = fmax(0.0, q / n - mean * mean);
-      gmean[g] = static_cast<float>(mean);
-      ginv[g] = static_cast<float>(1.0 / sqrt(var + 1e-5));
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = tid + i * kUpdThreads;
-    if (c < C) {
-      const int g = c / cpg;
-      const float scale = ginv[g] * op.gamma[c];
-      const float shift = op.beta[c];
-      const float mean = gmean[g];
-#pragma unroll
-      for (int t = 0; t < H; ++t) hv[i][t] = mish_fast(fmaf(hv[i][t] - mean, scale, shift));
-    }
-  }
-  for (int a0 = 0; a0 < A; a0 += AG) {
-    float p[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) p[v] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = tid + i * kUpdThreads;
-      if (c < C) {
-#pragma unroll
-        for (int aa = 0; aa < AG; ++aa) {
-          const int a = a0 + aa;
-          const float w = a0 == 0 ? w0[aa][i]
-                                  : (a < A ? op.wo[static_cast<std::int64_t>(a) * C + c] : 0.0f);
-#pragma unroll
-          for (int t = 0; t < H; ++t) p[aa * H + t] = fmaf(w, hv[i][t], p[aa * H + t]);
-        }
-      }
-    }
-    rs_step<V, 32>(p, lane);
-    const int off = rs_offset<V>(lane);
-    if (rs_writer<V>(lane)) red[wave][off] = p[0];
-    __syncthreads();
-    if (tid < V) {
-      float s = 0.0f;
-      for (int w = 0; w < kUpdThreads / kWave; ++w) s += red[w][tid];
-      const int a = a0 + tid / H;
-      if (a < A) eps[a][tid % H] = s + op.bo[a];
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int r = 0; r < XPL; ++r) {
-    const int i = tid + r * kUpdThreads;
-    if (i >= A * H) break;
-    apply_update(op, sample, i / H, i % H, A, H, eps[i / H][i % H], xs[r]);  // state [A][H]
-  }
+__global__ __launch_bounds__(upd::kUpdThreads) void update_kernel(UpdateOp op) {
+  __shared__ upd::UpdateSmem<H> sm;
+  upd::update_body<H, false>(op, blockIdx.x, gridDim.x, sm);
 }
 
 // Shapes outside update_kernel's instances: one wavefront per output value eps[a][t] (lanes
@@ -424,7 +210,7 @@ __global__ __launch_bounds__(kUpdGenThreads) void update_general_kernel(UpdateOp
     for (int m = kWave / 2; m >= 1; m >>= 1) p += __shfl_xor(p, m, kWave);
     if (lane == 0) {
       const float xv = op.kind != kUpdateDenoise ? op.x[sample + o] : 0.0f;
-      apply_update(op, sample, a, t, A, H, p + op.bo[a], xv);
+      upd::apply_update<false>(op, sample, gridDim.x, a, t, A, H, p + op.bo[a], xv);
     }
   }
 }
@@ -477,8 +263,8 @@ hipError_t begin_sample(const float* noise, float* x, float* xin, int batch, int
 
 namespace {
 bool update_fused_ok(int c0, int groups, int horizon, int action_dim) {
-  return c0 <= kUpdThreads * kMaxUpdateChannelsPerLane && groups <= kMaxUpdateGroups &&
-         action_dim <= kMaxActions &&
+  return c0 <= upd::kUpdThreads * upd::kMaxUpdateChannelsPerLane && groups <= upd::kMaxUpdateGroups &&
+         action_dim <= upd::kMaxActions &&
          (horizon == 1 || horizon == 2 || horizon == 4 || horizon == 8 || horizon == 16);
 }
 }  // namespace
@@ -492,11 +278,11 @@ hipError_t update(const UpdateOp& op, int batch, hipStream_t stream) {
     return hipGetLastError();
   }
   switch (op.horizon) {
-    case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
-    case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
-    case 4: hipLaunchKernelGGL(update_kernel<4>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
-    case 8: hipLaunchKernelGGL(update_kernel<8>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
-    default: hipLaunchKernelGGL(update_kernel<16>, dim3(batch), dim3(kUpdThreads), 0, stream, op); break;
+    case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 4: hipLaunchKernelGGL(update_kernel<4>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 8: hipLaunchKernelGGL(update_kernel<8>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    default: hipLaunchKernelGGL(update_kernel<16>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
   }
   return hipGetLastError();
 }

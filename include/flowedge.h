@@ -314,6 +314,17 @@ int fe_engine_prepare(fe_engine* engine, int kind, size_t batch, size_t steps, i
  * resumable-solve graphs). */
 uint64_t fe_engine_graph_captures(const fe_engine* engine);
 
+/* 1 when this engine runs batch-1 sampling ticks (up to 128 U-Net evaluations) as one persistent
+ * kernel launch (one workgroup per compute unit, convolution steps handed over through
+ * device-coherent memory), 0 when they run as a graph of per-layer launches (the default).  Both
+ * compute the same values.  FLOWEDGE_PERSISTENT=1 in the environment at load selects the
+ * persistent kernel.  If a persistent tick is ever abandoned (not every workgroup became
+ * resident), the engine re-runs that call on the per-layer graphs and keeps using them. */
+int fe_engine_persistent_tick(const fe_engine* engine);
+
+/* Why fe_engine_persistent_tick is 0 ("" when it is 1). */
+const char* fe_engine_persistent_tick_reason(const fe_engine* engine);
+
 /* Largest batch the arena was sized for (FLOWEDGE_MAX_BATCH at load, default 256). */
 size_t fe_engine_max_batch(const fe_engine* engine);
 
