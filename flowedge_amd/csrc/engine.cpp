@@ -259,6 +259,16 @@ struct FeEngine {
   int blocks = 0;  // residual blocks (Work buffer ids 0 .. blocks-1)
   std::size_t max_nfe = 0;
   std::size_t ddim_table = 0;  // FiLM time rows for every train timestep [T][F] (epsilon models)
+  // Velocity models: FiLM time rows of the flow solves sampled so far, per (steps, method), in a
+  // pool of flow_pool_rows rows [row][F] (DDIM's table counterpart; the solve's evaluation times
+  // depend on its step count and method).
+  struct FlowTable {
+    std::size_t steps = 0;
+    int method = 0;
+    std::size_t row0 = 0;
+  };
+  std::size_t flow_pool = 0, flow_pool_rows = 0, flow_pool_used = 0;
+  std::vector<FlowTable> flow_tables;
   std::size_t mfma_batch = 5;  // batches of at least this many samples use the matrix cores
   bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
   bool f32_split = false;      // F32 weights on the BF16 matrix cores (split weights and input)
@@ -350,6 +360,9 @@ constexpr std::size_t kGraphCache = 32;
 // (longer solves run on per-layer graphs).
 constexpr std::size_t kChainTables = kGraphCache;
 constexpr std::size_t kMaxChainEvals = 128;
+// Velocity models: FiLM time rows kept for flow solves (RK4-4 takes 16, Euler-10 10; pusht-size
+// rows are 115 KB each).
+constexpr std::size_t kFlowPoolRows = 256;
 
 void end_solve(FeEngine* e);
 
@@ -499,6 +512,10 @@ struct Builder {
     e.film_wc = plan.take(c.cond_dim * F * 4);
     e.film_bias = plan.take(F * 4);
     if (c.prediction == 0) e.ddim_table = plan.take(c.train_timesteps * F * 4);
+    if (c.prediction == 1) {
+      e.flow_pool_rows = kFlowPoolRows;
+      e.flow_pool = plan.take(kFlowPoolRows * F * 4);
+    }
     // U-Net evaluations per call: diffusion <= T steps, flow RK4 4 per step.
     e.max_nfe = std::max<std::size_t>(c.train_timesteps, 1024);
     // Persistent tick: step table, per-workgroup counters and state slots (x, xin and four flow
@@ -1176,17 +1193,20 @@ hipError_t enqueue_diffusion(FeEngine& e, int batch, std::size_t steps, int sche
   return enqueue_diffusion_readout(e, batch);
 }
 
-// Flow-ODE sampling (flow.cc:291-318) with the U-Net as velocity field, in the same three parts:
-// the start also computes the FiLM time rows of every evaluation of the solve.
+// Flow-ODE sampling (flow.cc:291-318) with the U-Net as velocity field, in the same three parts.
+// `film` holds the FiLM time rows of every evaluation of the solve (flow_table); when it is null
+// the start computes them into the workspace.
 std::size_t flow_stages(int method) {
   return method == FE_SOLVER_RK4 ? 4 : (method == FE_SOLVER_HEUN ? 2 : 1);
 }
 
-hipError_t enqueue_flow_start(FeEngine& e, int batch, std::size_t steps, int method) {
+hipError_t enqueue_flow_start(FeEngine& e, int batch, std::size_t steps, int method,
+                              const float* film) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   FE_TRY(begin_sample(e.wp(e.w.in_noise), e.wp(e.w.x_state), e.wp(e.w.x_in), batch,
                       static_cast<int>(c.horizon), static_cast<int>(c.action_dim), e.stream));
+  if (film != nullptr) return enqueue_film_cond(e, batch);
   TimeSpec ts;
   ts.mode = kTimesFlow;
   ts.steps = static_cast<int>(steps);
@@ -1229,13 +1249,18 @@ fe::hip::UpdateOp flow_update(FeEngine& e, std::size_t steps, int method, int j)
   }
 }
 
+// The FiLM time rows a solve reads: its table, or the workspace rows its start computes.
+const float* flow_rows(const FeEngine& e, const float* film) {
+  return film != nullptr ? film : e.wp(e.w.film_table);
+}
+
 hipError_t enqueue_flow_step(FeEngine& e, int batch, std::size_t steps, int method,
-                             std::size_t step) {
+                             std::size_t step, const float* film) {
   const int stages = static_cast<int>(flow_stages(method));
   for (int j = 0; j < stages; ++j) {
     const fe::hip::UpdateOp u = flow_update(e, steps, method, j);
     const std::size_t n = step * static_cast<std::size_t>(stages) + static_cast<std::size_t>(j);
-    FE_TRY(enqueue_unet(e, batch, e.wp(e.w.film_table) + n * e.film_total, u));
+    FE_TRY(enqueue_unet(e, batch, flow_rows(e, film) + n * e.film_total, u));
   }
   return hipSuccess;
 }
@@ -1248,9 +1273,11 @@ hipError_t enqueue_flow_readout(FeEngine& e, int batch) {
                                 e.stream);
 }
 
-hipError_t enqueue_flow(FeEngine& e, int batch, std::size_t steps, int method) {
-  FE_TRY(enqueue_flow_start(e, batch, steps, method));
-  for (std::size_t s = 0; s < steps; ++s) FE_TRY(enqueue_flow_step(e, batch, steps, method, s));
+hipError_t enqueue_flow(FeEngine& e, int batch, std::size_t steps, int method,
+                        const float* film) {
+  FE_TRY(enqueue_flow_start(e, batch, steps, method, film));
+  for (std::size_t s = 0; s < steps; ++s)
+    FE_TRY(enqueue_flow_step(e, batch, steps, method, s, film));
   return enqueue_flow_readout(e, batch);
 }
 
@@ -1298,7 +1325,8 @@ std::size_t evaluations(int kind, std::size_t steps, int mode) {
 
 // Fills evaluation table `table` of the persistent tick for this solve: each evaluation's FiLM
 // time rows and the update after it, computed exactly as the per-layer graphs compute them.
-hipError_t fill_chain_table(FeEngine& e, int kind, std::size_t steps, int mode, int table) {
+hipError_t fill_chain_table(FeEngine& e, int kind, std::size_t steps, int mode, int table,
+                            const float* film) {
   using namespace fe::hip;
   const Config& c = e.cfg;
   std::vector<ChainEval> evals;
@@ -1319,7 +1347,7 @@ hipError_t fill_chain_table(FeEngine& e, int kind, std::size_t steps, int mode, 
         ChainEval ev;
         ev.upd = flow_update(e, steps, mode, j);
         update_base(e, ev.upd);
-        ev.film_row = e.wp(e.w.film_table) + (st * stages + j) * e.film_total;
+        ev.film_row = flow_rows(e, film) + (st * stages + j) * e.film_total;
         evals.push_back(ev);
       }
   }
@@ -1329,9 +1357,10 @@ hipError_t fill_chain_table(FeEngine& e, int kind, std::size_t steps, int mode, 
 
 // One batch-1 tick on the persistent kernel: the solve's start (noise into the state, FiLM rows),
 // the tick kernel, the readout, and a copy of the tick's abort flag to the host.
-hipError_t enqueue_chain_tick(FeEngine& e, int kind, std::size_t steps, int mode, int table) {
+hipError_t enqueue_chain_tick(FeEngine& e, int kind, std::size_t steps, int mode, int table,
+                              const float* film) {
   using namespace fe::hip;
-  FE_TRY(kind == 0 ? enqueue_diffusion_start(e, 1) : enqueue_flow_start(e, 1, steps, mode));
+  FE_TRY(kind == 0 ? enqueue_diffusion_start(e, 1) : enqueue_flow_start(e, 1, steps, mode, film));
   ChainTick t;
   t.steps = e.ptr<char>(e.chain_steps);
   t.nsteps = e.chain_nsteps;
@@ -1364,6 +1393,47 @@ void drop_chain_graphs(FeEngine& e) {
   }
 }
 
+// The FiLM time rows of a flow solve of `steps` steps with `method` (nullptr for diffusion
+// models and for solves with more evaluations than the pool holds; their graphs compute the rows).
+// Computed once per (steps, method) on the engine stream, outside any capture, and kept.  When
+// the pool is full it starts over, and the sampling graphs that read the old rows are dropped.
+hipError_t flow_table(FeEngine& e, std::size_t steps, int method, const float*& film) {
+  film = nullptr;
+  const std::size_t n = evaluations(1, steps, method);
+  if (e.flow_pool_rows == 0 || n > e.flow_pool_rows) return hipSuccess;
+  float* pool = e.ptr(e.flow_pool);
+  for (const FeEngine::FlowTable& t : e.flow_tables)
+    if (t.steps == steps && t.method == method) {
+      film = pool + t.row0 * e.film_total;
+      return hipSuccess;
+    }
+  if (e.flow_pool_used + n > e.flow_pool_rows) {
+    for (auto it = e.graphs.begin(); it != e.graphs.end();) {
+      if (it->kind == 1) {
+        (void)hipGraphExecDestroy(it->exec);
+        it = e.graphs.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    e.flow_tables.clear();
+    e.flow_pool_used = 0;
+  }
+  FeEngine::FlowTable t;
+  t.steps = steps;
+  t.method = method;
+  t.row0 = e.flow_pool_used;
+  fe::hip::TimeSpec ts;
+  ts.mode = fe::hip::kTimesFlow;
+  ts.steps = static_cast<int>(steps);
+  ts.method = method;
+  FE_TRY(enqueue_film_time(e, ts, static_cast<int>(n), pool + t.row0 * e.film_total));
+  e.flow_tables.push_back(t);
+  e.flow_pool_used += n;
+  film = pool + t.row0 * e.film_total;
+  return hipSuccess;
+}
+
 // Returns the cached graph for this shape, capturing it on first use.  Batch-1 solves of up to
 // kMaxChainEvals evaluations run as one persistent tick when the engine has a step table.
 hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps, int mode,
@@ -1382,6 +1452,8 @@ hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps
     (void)hipGraphExecDestroy(e.graphs.back().exec);
     e.graphs.pop_back();
   }
+  const float* film = nullptr;
+  if (kind == 1) FE_TRY(flow_table(e, steps, mode, film));
   int table = -1;
   if (chain) {
     std::vector<bool> used(kChainTables, false);
@@ -1389,18 +1461,18 @@ hipError_t get_graph(FeEngine& e, int kind, std::size_t batch, std::size_t steps
       if (g.chain_table >= 0) used[static_cast<std::size_t>(g.chain_table)] = true;
     for (std::size_t i = 0; i < kChainTables && table < 0; ++i)
       if (!used[i]) table = static_cast<int>(i);
-    FE_TRY(fill_chain_table(e, kind, steps, mode, table));
+    FE_TRY(fill_chain_table(e, kind, steps, mode, table, film));
   }
   hipGraphExec_t inst = nullptr;
   FE_TRY(capture_graph(
       e,
       [&]() {
-        if (chain) return enqueue_chain_tick(e, kind, steps, mode, table);
+        if (chain) return enqueue_chain_tick(e, kind, steps, mode, table, film);
         if (kind == 0) {
           const std::vector<float> alphas = alphas_cumprod(e.cfg.train_timesteps);
           return enqueue_diffusion(e, static_cast<int>(batch), steps, mode, alphas.data());
         }
-        return enqueue_flow(e, static_cast<int>(batch), steps, mode);
+        return enqueue_flow(e, static_cast<int>(batch), steps, mode, film);
       },
       inst));
   e.graphs.push_front(GraphEntry{kind, mode, batch, steps, inst, table});
@@ -1575,8 +1647,9 @@ hipError_t build_solve_graphs(FeEngine& e, int kind, std::size_t steps, int mode
                           : enqueue_diffusion_step(e, 1, steps, mode, alphas.data(), g - 1));
             return enqueue_diffusion_readout(e, 1);
           }
-          FE_TRY(g == 0 ? enqueue_flow_start(e, 1, steps, mode)
-                        : enqueue_flow_step(e, 1, steps, mode, g - 1));
+          // A solve computes its own rows (a later call may reset the table pool mid-solve).
+          FE_TRY(g == 0 ? enqueue_flow_start(e, 1, steps, mode, nullptr)
+                        : enqueue_flow_step(e, 1, steps, mode, g - 1, nullptr));
           return enqueue_flow_readout(e, 1);
         },
         exec);

@@ -125,6 +125,33 @@ def test_flow_resumable_matches_oracle_and_sample(flow_small):
             assert np.array_equal(out, whole)
 
 
+def test_flow_time_tables_across_pool_reset(flow_small):
+    # One-shot flow calls keep their FiLM time rows per (steps, method) in a 256-row pool; a call
+    # whose rows no longer fit starts the pool over and drops the graphs that read it.  Resumable
+    # solves compute their rows themselves, so each one-shot call must equal the stepped solve.
+    cond, x0 = ck.inputs(FLOW_SPEC)
+    shape = (FLOW_SPEC.horizon, FLOW_SPEC.action_dim)
+    with flowedge_amd.Engine(flow_small) as e:
+        def whole(method, steps):
+            out = np.empty(shape, np.float32)
+            e.sample_condition(cond[0], x0[0], out, steps=steps, method=method)
+            return out
+
+        def stepped(method, steps):
+            out = np.empty(shape, np.float32)
+            e.flow_begin(cond[0], x0[0], steps=steps, method=method)
+            assert e.flow_advance(out, steps) == 0
+            return out
+
+        first = whole("rk4", 4)
+        assert np.array_equal(first, stepped("rk4", 4))
+        for steps in (20, 21, 22, 23):  # 16 + 80 + 84 + 88 rows > 256: the pool starts over
+            say(f"flow rk4-{steps} one-shot vs stepped")
+            assert np.array_equal(whole("rk4", steps), stepped("rk4", steps))
+        assert np.array_equal(whole("rk4", 4), first)
+        assert np.array_equal(whole("euler", 10), stepped("euler", 10))
+
+
 def test_model_digest_matches_reference_fingerprint(tiny, tiny_engine, flow_small):
     want = fingerprint.fingerprint(tiny)
     assert tiny_engine.model_metadata["model_digest"] == want
