@@ -159,18 +159,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, unsig
 }
 
 // voff: byte offset of the row/chunk (or kOutOfRange); soff: wave-uniform byte offset of the tap.
+// Weights are read once per U-Net evaluation (about 1 GB for the pusht-size model, more than the
+// 256 MB MALL holds), so they are loaded non-temporal (cache policy nt): they then stop evicting
+// the activations the next layers read from L2 and MALL (B=1 DDIM-10 tick 3.49 -> 3.15 ms).
+constexpr int kWeightPolicy = 2;  // nt
+
 template <bool BF16>
 __device__ __forceinline__ void load_vec4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff,
                                           float* out) {
   if constexpr (BF16) {
-    const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kWeightPolicy);
     const uint2 raw = __builtin_bit_cast(uint2, t);
     out[0] = __uint_as_float(raw.x << 16);
     out[1] = __uint_as_float(raw.x & 0xffff0000u);
     out[2] = __uint_as_float(raw.y << 16);
     out[3] = __uint_as_float(raw.y & 0xffff0000u);
   } else {
-    const auto t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const auto t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kWeightPolicy);
     const float4 v = __builtin_bit_cast(float4, t);
     out[0] = v.x;
     out[1] = v.y;
