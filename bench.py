@@ -110,6 +110,7 @@ def conv_breakdown(eng, batch: int = 1, iters: int = 50):
     layers launched round-robin, on the kernels a call of this batch uses) and its share of an
     evaluation."""
     convs = eng.convolutions()
+    slices = eng.conv_slices(batch)
     groups = {}
     for c in convs:
         groups.setdefault(shape_of(c["name"]), []).append(c)
@@ -118,6 +119,7 @@ def conv_breakdown(eng, batch: int = 1, iters: int = 50):
         us = eng.time_convolutions([c["index"] for c in cs], batch=batch, iters=iters)
         nbytes = cs[0]["weight_bytes"] + cs[0]["sample_bytes"] * batch
         row = {"shape": shape, "launches_per_nfe": len(cs), "us_per_launch": round(us, 3),
+               "slices": sorted({slices[c["index"]] for c in cs}),
                "us_per_nfe": round(us * len(cs), 2), "bytes_per_launch": nbytes,
                "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "indices": [c["index"] for c in cs]}
         if batch > 1:
@@ -133,6 +135,10 @@ def dominant_roofline(eng, iters: int):
     if not convs:
         return None
     idx = [c["index"] for c in convs]
+    slices = sorted({eng.conv_slices(1)[i] for i in idx})
+    kernel = (f"conv_slice_kernel<kConvSame, K=5, LIN=4, kProFilm, RES=false> {DOMINANT_SHAPE}, "
+              f"{slices} input-channel slices" if slices != [1] else
+              f"conv_kernel<kConvSame, K=5, LIN=4, VEC=4, kProFilm, RES=false> {DOMINANT_SHAPE}")
     us = eng.time_convolutions(idx, batch=1, iters=iters)
     nbytes = convs[0]["weight_bytes"] + convs[0]["sample_bytes"]
     achieved = nbytes / (us * 1e-6) / 1e9
@@ -151,8 +157,7 @@ def dominant_roofline(eng, iters: int):
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
-        "kernel": "conv_kernel<kConvSame, K=5, LIN=4, VEC=4, kProFilm, RES=false, NC=4> "
-                  + DOMINANT_SHAPE,
+        "kernel": kernel,
         "algorithmic_bytes_per_launch": nbytes,
         "us_per_launch": round(us, 3),
         "launches_timed": iters * len(idx),
@@ -364,8 +369,8 @@ def main():
         rows = conv_breakdown(eng, batch=int(batch), iters=10)
         for r in rows:
             print(f"[bench] {work} B={batch} {r['shape']:36s} x{r['launches_per_nfe']} "
-                  f"{r['us_per_launch']:9.2f} us {r.get('tflops', 0):7.1f} TFLOP/s", file=sys.stderr,
-                  flush=True)
+                  f"{r['us_per_launch']:9.2f} us {r.get('tflops', 0):7.1f} TFLOP/s "
+                  f"slices {r['slices']}", file=sys.stderr, flush=True)
         print(json.dumps({"breakdown": work, "batch": int(batch),
                           "rows": [{k: v for k, v in r.items() if k != "indices"} for r in rows]}),
               flush=True)

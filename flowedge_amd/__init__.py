@@ -37,7 +37,8 @@ EXPORTS = [
     "fe_engine_flow_begin_request", "fe_engine_cancel_before", "fe_engine_flow_advance",
     "fe_engine_flow_action_metadata", "fe_engine_diffusion_begin",
     "fe_engine_diffusion_begin_generation", "fe_engine_diffusion_advance",
-    "fe_weights_model_digest", "fe_engine_conv_path", "fe_engine_graph_captures",
+    "fe_weights_model_digest", "fe_engine_conv_path", "fe_engine_conv_slices",
+    "fe_engine_graph_captures",
     "fe_engine_diffusion_denoise_noalloc", "fe_engine_persistent_tick",
     "fe_engine_persistent_tick_reason",
 ]
@@ -141,6 +142,7 @@ def lib():
     L.fe_engine_time_convs.argtypes = [vp, ctypes.POINTER(sz), sz, sz, sz,
                                        ctypes.POINTER(ctypes.c_float)]
     L.fe_engine_conv_path.argtypes = [vp, sz, sz, ctypes.POINTER(cint)]
+    L.fe_engine_conv_slices.argtypes = [vp, sz, sz, ctypes.POINTER(cint)]
     L.fe_engine_flow_begin.argtypes = [vp, _f32p, _f32p, sz, cint]
     L.fe_engine_make_condition_metadata.argtypes = [vp, u64, u64, u64, sz, cint,
                                                     ctypes.POINTER(ConditionMetadata)]
@@ -479,6 +481,19 @@ class Engine:
         for i in range(n.value):
             self._check(L.fe_engine_conv_path(self._h, i, batch, ctypes.byref(p)))
             out.append(names[p.value])
+        return out
+
+    def conv_slices(self, batch: int = 1) -> list[int]:
+        """Input-channel slices each convolution of convolutions() runs with at `batch` (1:
+        unsliced)."""
+        L = lib()
+        n = ctypes.c_size_t()
+        self._check(L.fe_engine_conv_count(self._h, ctypes.byref(n)))
+        out = []
+        p = ctypes.c_int()
+        for i in range(n.value):
+            self._check(L.fe_engine_conv_slices(self._h, i, batch, ctypes.byref(p)))
+            out.append(p.value)
         return out
 
     def time_convolutions(self, indices, batch: int = 1, iters: int = 100) -> float:

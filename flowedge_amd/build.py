@@ -18,6 +18,9 @@ LIB = os.path.join(HERE, "libflowedge_amd.so")
 OBJDIR = os.path.join(HERE, "_build")
 SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/conv_fused.hip",
            "csrc/conv_same5.hip", "csrc/conv_same3.hip", "csrc/conv_resample.hip",
+           "csrc/conv_slice.hip", "csrc/conv_slice_s16.hip", "csrc/conv_slice_l16.hip",
+           "csrc/conv_slice_s32.hip", "csrc/conv_slice_l32.hip", "csrc/conv_slice_s64.hip",
+           "csrc/conv_slice_l64.hip",
            "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/conv_general.hip",
            "csrc/identity.cpp", "csrc/scratch.hip", "csrc/chain.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -97,7 +97,65 @@ bool fused_plan(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, Vie
   return true;
 }
 
+// Plan of the sliced kernel with S input-channel slices: each slice holds whole GroupNorm groups
+// of the normalised part (or lies in the plain part), stages at most kSliceFloats floats, and
+// the rows (slice_tpr lanes) fit the chunk budget.  Tiles of a slice are spread over at most
+// kMaxBlocks / S workgroups.
+bool plan_slices(const ConvOp& op, bool res, const ConvInput& in, int S, int tpr, LaunchPlan& p) {
+  if (!slice_instance(op.mode, op.k, op.lin, res)) return false;
+  if (tpr != 16 && tpr != 32 && tpr != 64) return false;
+  if (!slice_tpr_ok(op.mode, op.lin, res, tpr)) return false;
+  if (S < 2 || S > kMaxSlices || op.ic % S != 0) return false;
+  const int ics = op.ic / S;
+  if (ics % 4 != 0 || ics * op.lin > kSliceFloats || in.split % ics != 0) return false;
+  if (in.norm && ics % (in.split / in.groups) != 0) return false;
+  if (in.parts < 1 || in.parts > kMaxSlices || in.res_parts < 1 || in.res_parts > kMaxSlices)
+    return false;
+  const int nch = (ics / 4 + tpr - 1) / tpr;
+  if (nch > slice_budget(op.k, op.lin, res, tpr)) return false;
+  p.vec = 4;
+  p.tpr = tpr;
+  p.nch = nch;
+  const int rpt = kThreads / tpr;
+  p.tiles = (op.oc + rpt - 1) / rpt;
+  const int cap = kMaxBlocks / S;                    // workgroups per slice
+  const int per = (p.tiles + cap - 1) / cap;         // tiles per workgroup
+  p.blocks = (p.tiles + per - 1) / per;
+  return true;
+}
+
+ConvInput single_part(ConvInput in) {
+  in.parts = 1;
+  in.res_parts = 1;
+  return in;
+}
+
 }  // namespace
+
+SlicePlan conv_fused_slices(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr,
+                            int batch, int max_slices, int tpr) {
+  SlicePlan best;
+  LaunchPlan p;
+  if (!fused_plan(op, res1x1, single_part(in), yr, batch, p) || p.vec != 4) return best;
+  // The most slices with any lane count; among lane counts, the most workgroups (up to one per
+  // CU), then the fewest lanes per row (more weight chunks in flight per lane).
+  for (int S = kMaxSlices; S >= 2; S /= 2) {
+    if (S > max_slices) continue;
+    int wgs = 0;
+    for (int t = 16; t <= 64; t *= 2) {
+      LaunchPlan q;
+      if ((tpr != 0 && t != tpr) || !plan_slices(op, res1x1 != nullptr, in, S, t, q)) continue;
+      const int n = q.blocks * S;
+      if (n > wgs) {
+        wgs = n;
+        best.slices = S;
+        best.tpr = t;
+      }
+    }
+    if (wgs > 0) return best;
+  }
+  return best;
+}
 
 bool conv_fused_supported(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr,
                           int batch) {
@@ -145,10 +203,30 @@ bool fused_args(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, Vie
 }  // namespace conv
 
 hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
-                      View yr, int batch, hipStream_t stream) {
+                      View yr, int batch, hipStream_t stream, SlicePlan sp) {
   const bool res = res1x1 != nullptr;
   Args a;
   int vec = 4, pro = 0;
+  const int slices = sp.slices;
+  if (slices > 1) {
+    // The unsliced checks, then the slice plan.
+    LaunchPlan p;
+    if (!conv::fused_args(op, res1x1, single_part(in), y, yr, batch, a, vec, pro) || vec != 4 ||
+        !plan_slices(op, res, in, slices, sp.tpr, p))
+      return hipErrorInvalidValue;
+    a.in = in;
+    a.slices = slices;
+    a.ics = op.ic / slices;
+    a.tpr = p.tpr;
+    a.nch = p.nch;
+    a.tiles = p.tiles;
+    a.blocks = p.blocks;
+    a.ypart = y.part;
+    a.yrpart = yr.part;
+    return launch_slice(op.mode, op.k, op.lin, pro, res, a, batch, stream);
+  }
+  // The unsliced kernel reads single tensors only.
+  if (in.parts != 1 || in.res_parts != 1) return hipErrorInvalidValue;
   if (!conv::fused_args(op, res1x1, in, y, yr, batch, a, vec, pro)) return hipErrorInvalidValue;
   if (op.mode == kConvSame)
     return op.k == 5 ? launch_same5(op.lin, vec, pro, res, a, batch, stream)

@@ -89,6 +89,13 @@ struct Args {
   int blocks;  // workgroups (grid.x); workgroup g takes tiles g, g + blocks, ...
   int tpr;     // lanes per row
   int nch;     // chunks per lane (<= chunk_budget)
+  // Input-channel slices (sliced kernel only): grid.x = blocks * slices; workgroup x takes slice
+  // x % slices and, within it, tiles x / slices, + blocks, ... of `tiles`; it stages channels
+  // [slice * ics, +ics) and writes the partial sum of that slice to y + slice * ypart (bias in
+  // slice 0 only).
+  int slices = 1;
+  int ics = 0;
+  std::int64_t ypart = 0, yrpart = 0;
   ConvInput in;
 };
 
@@ -185,18 +192,21 @@ __device__ __forceinline__ void load_vec4(__amdgpu_buffer_rsrc_t r, unsigned vof
 }
 
 // Weights of one input chunk (all taps, then the projection tap) of one row.
+// `c0`: first input channel of the workgroup's slice (0 unsliced).
 template <int K, int VEC, bool RES, bool BF16>
 __device__ __forceinline__ void load_chunk(const Args& a, __amdgpu_buffer_rsrc_t wr,
                                            __amdgpu_buffer_rsrc_t rr, int row, int cv, bool valid,
-                                           float (&w)[K + (RES ? 1 : 0)][VEC]) {
+                                           float (&w)[K + (RES ? 1 : 0)][VEC], int c0 = 0) {
   if constexpr (VEC == 4) {
     constexpr unsigned es = BF16 ? 2u : 4u;
-    const unsigned voff = valid ? static_cast<unsigned>(row * K * a.ic + cv * 4) * es : kOutOfRange;
+    const unsigned voff =
+        valid ? static_cast<unsigned>(row * K * a.ic + c0 + cv * 4) * es : kOutOfRange;
 #pragma unroll
     for (int k = 0; k < K; ++k)
       load_vec4<BF16>(wr, voff, static_cast<unsigned>(k * a.ic) * es, w[k]);
     if constexpr (RES) {
-      const unsigned roff = valid ? static_cast<unsigned>(row * a.ic + cv * 4) * es : kOutOfRange;
+      const unsigned roff =
+          valid ? static_cast<unsigned>(row * a.ic + c0 + cv * 4) * es : kOutOfRange;
       load_vec4<BF16>(rr, roff, 0u, w[K]);
     }
   } else {
@@ -451,6 +461,170 @@ __device__ __forceinline__ void stage_finish(const Args& a, int b, int wg, Stage
   lds_barrier();
 }
 
+// ---- Sliced prologue: the workgroup's slice of the input, one 16-byte chunk per lane ----
+//
+// Slice `sl` covers channels [c0, c0 + ics), c0 = sl * ics, wholly inside the normalised part
+// [0, split) or wholly inside the plain part (the planner aligns slices with `split` and with the
+// GroupNorm groups), so every statistic the slice needs is a sum over its own chunks.
+template <int LIN, int PRO>
+struct SliceRegs {
+  static constexpr int NPC = LIN >= 4 ? 1 : 4 / LIN;  // channels per chunk
+  float4 x;
+  float4 r;
+  float gam[NPC], bet[NPC];
+  float ts[PRO == kProFilm ? NPC : 1], cs[PRO == kProFilm ? NPC : 1];
+  float tb[PRO == kProFilm ? NPC : 1], cb[PRO == kProFilm ? NPC : 1];
+};
+
+// Sum of the partials p < n of a sliced producer's output at p (consecutive partials `stride`
+// floats apart), added in order p = 0, 1, ...; every load is issued before the first add.
+__device__ __forceinline__ float4 load_parts(const float* p, int n, std::int64_t stride) {
+  float4 v[kMaxSlices];
+#pragma unroll
+  for (int j = 0; j < kMaxSlices; ++j)
+    if (j < n) v[j] = *reinterpret_cast<const float4*>(p + j * stride);
+  float4 s = v[0];
+#pragma unroll
+  for (int j = 1; j < kMaxSlices; ++j)
+    if (j < n) s = float4{s.x + v[j].x, s.y + v[j].y, s.z + v[j].z, s.w + v[j].w};
+  return s;
+}
+
+template <int LIN, int PRO>
+__device__ __forceinline__ void slice_issue(const Args& a, int b, int sl, SliceRegs<LIN, PRO>& s) {
+  using S = SliceRegs<LIN, PRO>;
+  const ConvInput& in = a.in;
+  const int c0 = sl * a.ics;
+  const int nq = a.ics * LIN / 4;
+  const int q = threadIdx.x;
+  s.x = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  s.r = s.x;
+  if (q >= nq) return;
+  const std::int64_t e = static_cast<std::int64_t>(c0) * LIN + 4 * q;
+  if (c0 >= in.split) {
+    s.x = *reinterpret_cast<const float4*>(in.plain + b * in.plain_stride + e -
+                                           static_cast<std::int64_t>(in.split) * LIN);
+    return;
+  }
+  s.x = load_parts(in.src + b * in.src_stride + e, in.parts, in.part_stride);
+  if constexpr (PRO == kProResid)
+    s.r = load_parts(in.res + b * in.res_stride + e, in.res_parts, in.res_part_stride);
+  if constexpr (PRO != kProPlain) {
+    const float* ft = PRO == kProFilm ? in.film_time + in.film_off : nullptr;
+    const float* fc = PRO == kProFilm ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
+#pragma unroll
+    for (int i = 0; i < S::NPC; ++i) {
+      const int c = c0 + (4 * q) / LIN + i;
+      s.gam[i] = in.gamma[c];
+      s.bet[i] = in.beta[c];
+      if constexpr (PRO == kProFilm) {
+        s.ts[i] = ft[c];
+        s.cs[i] = fc[c];
+        s.tb[i] = ft[in.split + c];
+        s.cb[i] = fc[in.split + c];
+      }
+    }
+  }
+}
+
+// Statistics of the slice's groups, transform, materialisation (workgroup wt of `a.blocks` of
+// the slice writes chunks q with q % blocks == wt) and LDS staging.  `wsum` holds
+// 2 * kMaxGroups doubles (sums, then sums of squares).
+template <int LIN, int PRO>
+__device__ __forceinline__ void slice_finish(const Args& a, int b, int sl, int wt,
+                                             SliceRegs<LIN, PRO>& s, float* xs, double* wsum) {
+  using S = SliceRegs<LIN, PRO>;
+  const ConvInput& in = a.in;
+  const int c0 = sl * a.ics;
+  const int nq = a.ics * LIN / 4;
+  const int nv = a.ics / 4;
+  const int q = threadIdx.x;
+  const int lane = q & (kWave - 1);
+  if (PRO != kProPlain && c0 < in.split) {
+    const int npg = in.split / in.groups * LIN / 4;  // chunks per group
+    double sum = 0.0, sq = 0.0;
+    if (q < nq) {
+      const double d0 = s.x.x, d1 = s.x.y, d2 = s.x.z, d3 = s.x.w;
+      sum = (d0 + d1) + (d2 + d3);
+      sq = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    double gsum = 0.0, gsq = 0.0;
+    if (npg % kWave == 0) {
+      // Each wavefront lies in one group: wavefront sums, then the group's wavefronts in order.
+      sum = wave_sum(sum);
+      sq = wave_sum(sq);
+      if (lane == 0) {
+        wsum[q / kWave] = sum;
+        wsum[kMaxGroups + q / kWave] = sq;
+      }
+      lds_barrier();
+      if (q < nq) {
+        const int w0 = q / npg * (npg / kWave);
+        for (int i = 0; i < npg / kWave; ++i) {
+          gsum += wsum[w0 + i];
+          gsq += wsum[kMaxGroups + w0 + i];
+        }
+      }
+    } else {
+      // Small groups: per-chunk partials in LDS (aliased over xs, written again only after the
+      // next barrier), then one 16-lane row per group.
+      double* ps = reinterpret_cast<double*>(xs);
+      double* pq = ps + nq;
+      if (q < nq) {
+        ps[q] = sum;
+        pq[q] = sq;
+      }
+      lds_barrier();
+      const int g = q >> 4, sub = q & 15;
+      const int ng = nq / npg;
+      double rs = 0.0, rq = 0.0;
+      if (g < ng)
+        for (int i = sub; i < npg; i += 16) {
+          rs += ps[g * npg + i];
+          rq += pq[g * npg + i];
+        }
+      rs = row_sum(rs);
+      rq = row_sum(rq);
+      if (sub == 0 && g < ng) {
+        wsum[g] = rs;
+        wsum[kMaxGroups + g] = rq;
+      }
+      lds_barrier();
+      if (q < nq) {
+        gsum = wsum[q / npg];
+        gsq = wsum[kMaxGroups + q / npg];
+      }
+    }
+    if (q < nq) {
+      const double n = 4.0 * npg;
+      const double mean = gsum / n;
+      const double var = fmax(0.0, gsq / n - mean * mean);
+      const float fmean = static_cast<float>(mean);
+      const float inv = static_cast<float>(1.0 / sqrt(var + 1e-5));
+      float v[4] = {s.x.x, s.x.y, s.x.z, s.x.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = LIN >= 4 ? 0 : i / LIN;  // channel of element i within the chunk
+        float val = mish_fast(fmaf(v[i] - fmean, inv * s.gam[k], s.bet[k]));
+        if constexpr (PRO == kProFilm) val = fmaf(s.ts[k] + s.cs[k], val, s.tb[k] + s.cb[k]);
+        v[i] = val;
+      }
+      if constexpr (PRO == kProResid) {
+        v[0] += s.r.x;
+        v[1] += s.r.y;
+        v[2] += s.r.z;
+        v[3] += s.r.w;
+      }
+      s.x = float4{v[0], v[1], v[2], v[3]};
+      if (in.mat != nullptr && q % a.blocks == wt)
+        *reinterpret_cast<float4*>(in.mat + b * in.mat_stride + static_cast<std::int64_t>(c0) * LIN +
+                                   4 * q) = s.x;
+    }
+  }
+  if (q < nq) write_chunk<LIN>(xs, nv, q, s.x);
+  lds_barrier();
+}
+
 // The wait of a stand-alone launch: the stream order has already made the input visible.
 struct NoWait {
   __device__ bool operator()() const { return true; }
@@ -460,8 +634,24 @@ struct NoWait {
 // the persistent tick kernel) it starts with `wait()` (a workgroup-uniform call that returns once
 // the producers of the input have finished, false if the launch is being abandoned), and the
 // input and all outputs use device-coherent accesses.
+// Weight chunks per lane the registers allow (as chunk_budget, without the staging bound).
+__host__ __device__ constexpr int reg_chunks(int k, int lin, bool res) {
+  const int regs = lin >= 16 ? kWeightRegs - 64 : (lin >= 8 ? kWeightRegs - 32 : kWeightRegs);
+  const int n = regs / ((k + (res ? 1 : 0)) * 4);
+  return n < 8 ? n : 8;
+}
+
+// Lanes per row of the sliced kernel: 16, 32 or 64 (an instance parameter, chosen per
+// convolution by the planner), at least the reduced values per row.
+__host__ __device__ constexpr bool slice_tpr_ok(int mode, int lin, bool res, int tpr) {
+  return (res ? 2 : 1) * lout_of(mode, lin) <= tpr;
+}
+
+// SL (sliced kernel, stand-alone launches only): workgroup wg takes input-channel slice
+// wg % a.slices and row tiles wg / a.slices, + a.blocks, ...; rows are STPR lanes wide and
+// reduced within their lane segment.
 template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool BF16, int NC,
-          bool CHAIN = false, typename Wait = NoWait>
+          bool CHAIN = false, typename Wait = NoWait, bool SL = false, int STPR = 64>
 __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* xs, float* gmean,
                                           float* ginv, float* red, const Wait& wait = Wait{},
                                           Override ov = Override{}) {
@@ -469,16 +659,22 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
   constexpr int TAPS = K + (RES ? 1 : 0);
   constexpr int NCH = NC;  // chunk slots per lane: the plan's chunk count, or the budget
   constexpr int V = RES ? 2 * LOUT : LOUT;
+  static_assert(!SL || (VEC == 4 && !CHAIN && V <= STPR && STPR <= kWave),
+                "sliced: 16-byte chunks, stand-alone launches, one reduced value per lane");
   const int tid = threadIdx.x;
-  const int rpt = kThreads / a.tpr;  // rows per tile
-  const int gid = tid / a.tpr;
-  const int lg = tid - gid * a.tpr;
-  const int nv = a.ic / VEC;
+  const int tpr = SL ? STPR : a.tpr;
+  const int rpt = kThreads / tpr;  // rows per tile
+  const int gid = tid / tpr;
+  const int lg = tid - gid * tpr;
+  const int sl = SL ? wg % a.slices : 0;   // input-channel slice
+  const int c0 = SL ? sl * a.ics : 0;      // its first channel
+  const int nv = SL ? a.ics / 4 : a.ic / VEC;
   const int lane = tid & (kWave - 1);
+  if constexpr (SL) wg /= a.slices;        // workgroup index within the slice
 
   const __amdgpu_buffer_rsrc_t wr = buffer_of(a.w, a.wbytes);
   const __amdgpu_buffer_rsrc_t rr = buffer_of(RES ? a.rw : a.w, RES ? a.rwbytes : a.wbytes);
-  StageRegs<LIN, PRO> st;
+  std::conditional_t<SL, SliceRegs<LIN, PRO>, StageRegs<LIN, PRO>> st;
   if constexpr (CHAIN) {
     // The input is produced by other workgroups of this launch: wait for them first (a wait
     // issued behind weight loads would only complete once those arrive).  The parameters do not
@@ -486,7 +682,11 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
     if constexpr (VEC == 4) stage_params<LIN, PRO>(a, b, st, ov);
     if (!wait()) return false;
   }
-  if constexpr (VEC == 4) {
+  if constexpr (SL) {
+    slice_issue<LIN, PRO>(a, b, sl, st);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+  } else if constexpr (VEC == 4) {
     stage_issue<LIN, PRO, CHAIN>(a, b, st, ov);
     // Every wavefront's prologue reads are issued before any wavefront's weight loads: a CU's
     // vector memory path returns data in order, so an input read queued behind weight misses
@@ -507,18 +707,23 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
   const int row0 = tile * rpt + gid;
 #pragma unroll
   for (int j = 0; j < (EARLY < NCH ? EARLY : NCH); ++j) {
-    const int cv = lg + j * a.tpr;
-    load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j]);
+    const int cv = lg + j * tpr;
+    load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j],
+                                  c0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (VEC == 4) stage_finish<LIN, PRO, CHAIN>(a, b, wg, st, xs, gmean, ginv, ov);
+  if constexpr (SL)
+    slice_finish<LIN, PRO>(a, b, sl, wg, st, xs, reinterpret_cast<double*>(red));
+  else if constexpr (VEC == 4)
+    stage_finish<LIN, PRO, CHAIN>(a, b, wg, st, xs, gmean, ginv, ov);
 #pragma unroll
   for (int j = EARLY; j < NCH; ++j) {
-    const int cv = lg + j * a.tpr;
-    load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j]);
+    const int cv = lg + j * tpr;
+    load_chunk<K, VEC, RES, BF16>(a, wr, rr, row0, cv, j < a.nch && cv < nv && row0 < a.oc, w[j],
+                                  c0);
   }
 
-  const int waves = a.tpr / kWave;
+  const int waves = SL ? 1 : a.tpr / kWave;
   const int wig = lg / kWave;
   const float* xsrc = (ov.src != nullptr ? ov.src : a.in.src) + b * a.in.src_stride;
   int parity = 0;
@@ -533,7 +738,7 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int cv = lg + j * a.tpr;
+      const int cv = lg + j * tpr;
       const bool on = j < a.nch && cv < nv;
       if (on) {
         float xr[VEC][LIN];
@@ -589,15 +794,29 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
       // Refill this chunk's registers with the next tile's weights.
       if constexpr (decltype(refill)::value)
         load_chunk<K, VEC, RES, BF16>(a, wr, rr, nrow, cv, j < a.nch && cv < nv && nrow < a.oc,
-                                      w[j]);
+                                      w[j], c0);
     }
 
-    rs_step<V, 32>(acc, lane);
-    const int off = rs_offset<V>(lane);
     auto put = [&](float* p, float v) {
       if constexpr (CHAIN) st_dev(p, v);
       else *p = v;
     };
+    if constexpr (SL) {
+      // Rows of STPR lanes: reduce within the segment; slice sl writes its partial sum.
+      rs_step<V, STPR / 2>(acc, lane);
+      const int off = rs_offset_seg<V, STPR>(lane);
+      if (rs_writer_seg<V, STPR>(lane) && row < a.oc) {
+        if (!RES || off < LOUT)
+          put(a.y + b * a.ys + sl * a.ypart + static_cast<std::int64_t>(row) * LOUT + off,
+              sl == 0 ? acc[0] + a.bias[row] : acc[0]);
+        else
+          put(a.yr + b * a.yrs + sl * a.yrpart + static_cast<std::int64_t>(row) * LOUT + off - LOUT,
+              sl == 0 ? acc[0] + a.rbias[row] : acc[0]);
+      }
+      return;
+    }
+    rs_step<V, 32>(acc, lane);
+    const int off = rs_offset<V>(lane);
     if (waves == 1) {
       if (rs_writer<V>(lane) && row < a.oc) {
         if (!RES || off < LOUT)
@@ -648,6 +867,30 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(Args a) {
   }
 }
 
+// The sliced kernel: rows of TPR lanes over the workgroup's input-channel slice.
+template <int MODE, int K, int LIN, int PRO, bool RES, int NC, int TPR>
+__global__ __launch_bounds__(kThreads) void conv_slice_kernel(Args a) {
+  extern __shared__ float4 xs4[];
+  __shared__ double wsum[2 * kMaxGroups];
+  float* xs = reinterpret_cast<float*>(xs4);
+  float* red = reinterpret_cast<float*>(wsum);
+  const int wg = blockIdx.x, b = blockIdx.y;
+  if (a.bf16)
+    conv_body<MODE, K, LIN, 4, PRO, RES, true, NC, false, NoWait, true, TPR>(a, wg, b, xs, nullptr,
+                                                                             nullptr, red);
+  else
+    conv_body<MODE, K, LIN, 4, PRO, RES, false, NC, false, NoWait, true, TPR>(a, wg, b, xs,
+                                                                              nullptr, nullptr, red);
+}
+
+// Chunk slots per lane of the sliced kernel at TPR lanes per row: bounded by the weight
+// registers and by a slice of kSliceFloats staged floats.
+__host__ __device__ constexpr int slice_budget(int k, int lin, bool res, int tpr) {
+  const int by_regs = reg_chunks(k, lin, res);
+  const int by_size = (kSliceFloats / (lin * 4) + tpr - 1) / tpr;
+  return by_regs < by_size ? by_regs : by_size;
+}
+
 inline std::size_t stage_bytes(int ic, int lin, int vec) {
   if (vec != 4) return 0;
   const int planes = 4 * (lin >= 4 ? lin / 4 : 1);
@@ -655,8 +898,15 @@ inline std::size_t stage_bytes(int ic, int lin, int vec) {
 }
 constexpr std::size_t kMaxStageBytes = (kMaxStageFloats + 16 * kSwzPad) * sizeof(float);
 
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, int NC>
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, int NC, bool SL = false,
+          int TPR = 64>
 hipError_t launch_nc(const Args& a, int batch, hipStream_t s) {
+  if constexpr (SL) {
+    hipLaunchKernelGGL((conv_slice_kernel<MODE, K, LIN, PRO, RES, NC, TPR>),
+                       dim3(a.blocks * a.slices, batch), dim3(kThreads),
+                       stage_bytes(a.ics, LIN, 4), s, a);
+    return hipGetLastError();
+  }
   const std::size_t smem = stage_bytes(a.ic, LIN, VEC);
   auto fn = conv_kernel<MODE, K, LIN, VEC, PRO, RES, NC>;
   if (smem > 48 * 1024) {  // opt in to more than 48 KB of dynamic LDS (up to 160 KB per CU)
@@ -676,18 +926,22 @@ hipError_t launch_nc(const Args& a, int batch, hipStream_t s) {
 // Chunk slots per lane: the plan's count when it is 1, 2 or 4 (the common plans), otherwise the
 // register budget.  Slots beyond the plan's count still issue their (out-of-range, traffic-free)
 // loads, since the loads are branch-free, so exact counts save memory-pipeline issue slots.
-template <int MODE, int K, int LIN, int VEC, int PRO, bool RES>
+template <int MODE, int K, int LIN, int VEC, int PRO, bool RES, bool SL = false, int TPR = 64>
 hipError_t launch(const Args& a, int batch, hipStream_t s) {
-  constexpr int B = chunk_budget(K, LIN, RES, VEC);
-  if (a.nch == 1) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 1>(a, batch, s);
-  if constexpr (B > 2)
-    if (a.nch == 2) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 2>(a, batch, s);
-  if constexpr (B > 4)
-    if (a.nch == 4) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 4>(a, batch, s);
-  return launch_nc<MODE, K, LIN, VEC, PRO, RES, B>(a, batch, s);
+  if constexpr (SL && !slice_tpr_ok(MODE, LIN, RES, TPR)) {
+    return hipErrorInvalidValue;
+  } else {
+    constexpr int B = SL ? slice_budget(K, LIN, RES, TPR) : chunk_budget(K, LIN, RES, VEC);
+    if (a.nch == 1) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 1, SL, TPR>(a, batch, s);
+    if constexpr (B > 2)
+      if (a.nch == 2) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 2, SL, TPR>(a, batch, s);
+    if constexpr (B > 4)
+      if (a.nch == 4) return launch_nc<MODE, K, LIN, VEC, PRO, RES, 4, SL, TPR>(a, batch, s);
+    return launch_nc<MODE, K, LIN, VEC, PRO, RES, B, SL, TPR>(a, batch, s);
+  }
 }
 
-template <int MODE, int K, int LIN, int VEC>
+template <int MODE, int K, int LIN, int VEC, bool SL = false, int TPR = 64>
 hipError_t by_prologue(int pro, bool res, const Args& a, int batch, hipStream_t s) {
   if constexpr (VEC == 1) {
     if (pro == kProPlain && MODE == kConvSame)
@@ -696,20 +950,22 @@ hipError_t by_prologue(int pro, bool res, const Args& a, int batch, hipStream_t 
   } else if constexpr (MODE == kConvSame) {
     switch (pro) {
       case kProPlain:
-        return res ? launch<MODE, K, LIN, 4, kProPlain, true>(a, batch, s)
-                   : launch<MODE, K, LIN, 4, kProPlain, false>(a, batch, s);
+        return res ? launch<MODE, K, LIN, 4, kProPlain, true, SL, TPR>(a, batch, s)
+                   : launch<MODE, K, LIN, 4, kProPlain, false, SL, TPR>(a, batch, s);
       case kProFilm:
-        if (!res) return launch<MODE, K, LIN, 4, kProFilm, false>(a, batch, s);
+        if (!res) return launch<MODE, K, LIN, 4, kProFilm, false, SL, TPR>(a, batch, s);
         break;
       case kProResid:
-        return res ? launch<MODE, K, LIN, 4, kProResid, true>(a, batch, s)
-                   : launch<MODE, K, LIN, 4, kProResid, false>(a, batch, s);
+        return res ? launch<MODE, K, LIN, 4, kProResid, true, SL, TPR>(a, batch, s)
+                   : launch<MODE, K, LIN, 4, kProResid, false, SL, TPR>(a, batch, s);
       default:
         break;
     }
   } else {
-    if (!res && pro == kProPlain) return launch<MODE, K, LIN, 4, kProPlain, false>(a, batch, s);
-    if (!res && pro == kProResid) return launch<MODE, K, LIN, 4, kProResid, false>(a, batch, s);
+    if (!res && pro == kProPlain)
+      return launch<MODE, K, LIN, 4, kProPlain, false, SL, TPR>(a, batch, s);
+    if (!res && pro == kProResid)
+      return launch<MODE, K, LIN, 4, kProResid, false, SL, TPR>(a, batch, s);
   }
   return hipErrorInvalidValue;
 }
@@ -729,6 +985,17 @@ hipError_t by_lin(int lin, int pro, bool res, const Args& a, int batch, hipStrea
   return hipErrorInvalidValue;
 }
 
+// Sliced instances at TPR lanes per row for the lengths LINS (a.tpr selected the TPR).
+template <int MODE, int K, int TPR, int... LINS>
+hipError_t slice_lins(int lin, int pro, bool res, const Args& a, int batch, hipStream_t s) {
+  hipError_t st = hipErrorInvalidValue;
+  (void)((lin == LINS ? (st = by_prologue<MODE, K, LINS, 4, true, TPR>(pro, res, a, batch, s),
+                         true)
+                      : false) ||
+         ...);
+  return st;
+}
+
 // Host: the plan and arguments conv_fused launches with (false when it has no kernel for them);
 // `vec` and `pro` receive the instance's vector width and prologue kind.
 bool fused_args(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y, View yr,
@@ -746,5 +1013,10 @@ hipError_t launch_same5(int lin, int vec, int pro, bool res, const Args& a, int 
 hipError_t launch_same3(int lin, int vec, int pro, bool res, const Args& a, int batch,
                         hipStream_t s);
 hipError_t launch_resample(int mode, int lin, int pro, const Args& a, int batch, hipStream_t s);
+// The sliced kernel's instances (conv_slice*.hip): true when one exists for the shape; a.tpr
+// selects the lanes per row (16, 32 or 64).
+bool slice_instance(int mode, int k, int lin, bool res);
+hipError_t launch_slice(int mode, int k, int lin, int pro, bool res, const Args& a, int batch,
+                        hipStream_t s);
 
 }  // namespace fe::hip::conv

@@ -1,0 +1,12 @@
+// Kernel instances of the sliced fused convolution: K = 5 "same" convolutions at lengths 8 and
+// 16, 64 lanes per row.
+#include "conv_kernel.h"
+
+namespace fe::hip::conv {
+
+hipError_t launch_slice_same5_l64(int lin, int pro, bool res, const Args& a, int batch,
+                                  hipStream_t s) {
+  return slice_lins<kConvSame, 5, 64, 8, 16>(lin, pro, res, a, batch, s);
+}
+
+}  // namespace fe::hip::conv

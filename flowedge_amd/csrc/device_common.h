@@ -153,6 +153,29 @@ __device__ __forceinline__ bool rs_writer(int lane) {
   }
 }
 
+// The same for a reduce-scatter confined to SEG-lane segments (rs_step<N, SEG / 2>, N <= SEG):
+// the index of the finished sum a lane holds, and whether the lane is its segment's writer of it.
+template <int N, int SEG>
+__device__ __forceinline__ int rs_offset_seg(int lane) {
+  int off = 0, n = N;
+#pragma unroll
+  for (int m = SEG / 2; m >= 1; m >>= 1) {
+    if (n >= 2) {
+      if (lane & m) off += n / 2;
+      n /= 2;
+    }
+  }
+  return off;
+}
+template <int N, int SEG>
+__device__ __forceinline__ bool rs_writer_seg(int lane) {
+  if constexpr (N >= SEG) {
+    return true;
+  } else {
+    return (lane & (SEG / N - 1)) == 0;
+  }
+}
+
 // v + (v of lane l ^ 1), (l ^ 2), rotations by 4 and 8 within each 16-lane row, through DPP
 // moves of the two 32-bit halves (no LDS round trip).
 template <int CTRL>

@@ -55,6 +55,9 @@ bool env_flag(const char* name) {
 constexpr unsigned kMaxPoolThreads = 8;  // engine_runtime.h:39
 constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
 constexpr std::size_t kSplitKFloats = 1024 * 64 * 128;  // split-K partials: <= 1024 tiles of 64 x 128
+// Largest batch whose convolutions run input-channel sliced (on the fused kernels; the matrix
+// cores take over from 5 samples with F32 weights, 8 with BF16 weights).
+constexpr std::size_t kSliceBatch = 8;
 constexpr std::size_t kFinalNormGroups = 8;  // diffusion.cc:28
 constexpr std::size_t kAlign = 256;
 
@@ -194,6 +197,10 @@ struct Work {
   std::size_t seed = 0;                                    // DDPM seed (8 bytes)
   std::size_t concat[kMaxStages] = {};  // up stage u input [x ; skip] buffer [B][2*high][len]
   std::size_t ds_out[kMaxStages] = {};  // downsample outputs [B][C][len/2]
+  std::size_t us_out[kMaxStages] = {};  // sliced upsample outputs (partials) [B][S][C][2 len]
+  // Raw convolution outputs (h1, h2, r, ds_out, us_out, fconv_out) hold, for batches up to
+  // slice_batch, kMaxSlices partial sums per sample ([B][kMaxSlices][C][L]).
+  std::size_t slice_batch = 0;
   std::size_t h1[kMaxBlocks] = {}, h2[kMaxBlocks] = {};  // raw conv outputs [B][oc][len]
   std::size_t r[kMaxBlocks] = {};     // residual projection [B][oc][len] (non-identity blocks)
   std::size_t xmat[kMaxBlocks] = {};  // materialised block input [B][ic][len] (identity blocks)
@@ -270,6 +277,13 @@ struct FeEngine {
   std::size_t flow_pool = 0, flow_pool_rows = 0, flow_pool_used = 0;
   std::vector<FlowTable> flow_tables;
   std::size_t mfma_batch = 5;  // batches of at least this many samples use the matrix cores
+  // Input-channel slicing of the fused convolutions (batches below mfma_batch, up to the Work's
+  // slice_batch): on when every convolution of the model runs fused and the final update sums
+  // partials; slice_max (FLOWEDGE_SLICES, default kMaxSlices; 1 turns slicing off) caps it.
+  bool slice_ok = false;
+  int slice_max = fe::hip::kMaxSlices;
+  int slice_tpr = 0;  // lanes per row of the sliced kernels (FLOWEDGE_SLICE_TPR; 0: per shape)
+  bool records_sliced = false;  // conv_records were listed with slicing
   bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
   bool f32_split = false;      // F32 weights on the BF16 matrix cores (split weights and input)
 
@@ -317,6 +331,7 @@ struct FeEngine {
     fe::hip::ConvOp res;
     fe::hip::ConvInput in;
     fe::hip::View y, yr;
+    fe::hip::SlicePlan slices;
     std::uint64_t weight_bytes = 0;  // weights + biases
     std::uint64_t sample_bytes = 0;  // activations and per-channel parameters, per sample
   };
@@ -559,21 +574,25 @@ Work plan_work(const FeEngine& e, std::size_t batch, std::size_t rows, std::size
     const Block& r0 = e.up[u][0];
     w.concat[u] = plan.take(B * r0.ic * r0.len * 4);
   }
+  w.slice_batch = std::min(B, kSliceBatch);
+  const std::size_t PB = std::max(B, static_cast<std::size_t>(fe::hip::kMaxSlices) * w.slice_batch);
   auto acts = [&](const Block& blk) {
-    w.h1[blk.id] = plan.take(B * blk.oc * blk.len * 4);
-    w.h2[blk.id] = plan.take(B * blk.oc * blk.len * 4);
-    if (!blk.identity) w.r[blk.id] = plan.take(B * blk.oc * blk.len * 4);
+    w.h1[blk.id] = plan.take(PB * blk.oc * blk.len * 4);
+    w.h2[blk.id] = plan.take(PB * blk.oc * blk.len * 4);
+    if (!blk.identity) w.r[blk.id] = plan.take(PB * blk.oc * blk.len * 4);
     else w.xmat[blk.id] = plan.take(B * blk.ic * blk.len * 4);
   };
   for (std::size_t s = 0; s < c.stages; ++s) {
     for (int k = 0; k < 2; ++k) acts(e.down[s][k]);
-    if (s + 1 < c.stages) w.ds_out[s] = plan.take(B * c.dims[s] * (e.down[s][1].len / 2) * 4);
+    if (s + 1 < c.stages) w.ds_out[s] = plan.take(PB * c.dims[s] * (e.down[s][1].len / 2) * 4);
   }
   for (int m = 0; m < 2; ++m) acts(e.mid[m]);
-  for (std::size_t u = 0; u + 1 < c.stages; ++u)
+  for (std::size_t u = 0; u + 1 < c.stages; ++u) {
     for (int k = 0; k < 2; ++k) acts(e.up[u][k]);
+    w.us_out[u] = plan.take(PB * e.us[u].op.oc * e.us[u].op.lout * 4);
+  }
   w.final_in = plan.take(B * c.dims[0] * c.horizon * 4);
-  w.fconv_out = plan.take(B * c.dims[0] * c.horizon * 4);
+  w.fconv_out = plan.take(PB * c.dims[0] * c.horizon * 4);
   // Largest normalised activation (width * length of any block output).
   std::size_t norm_floats = 0;
   for (std::size_t st = 0; st < c.stages; ++st)
@@ -742,16 +761,17 @@ void bind_all(FeEngine& e) {
 
 hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
                          const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
-                         int batch, hipStream_t s);
+                         int batch, hipStream_t s, fe::hip::SlicePlan slices = {});
 enum class ConvPath : int { kFused = 0, kMatrix = 1, kGeneral = 2 };
 ConvPath conv_path(const FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
                    const fe::hip::ConvInput& in, fe::hip::View yr, int batch);
 
-// Launches one fused convolution; while recording, also keeps its arguments and algorithmic
-// bytes (each weight and bias once, each activation and per-channel parameter once per sample).
+// Launches one fused convolution (`slices` input-channel slices); while recording, also keeps its
+// arguments and algorithmic bytes (each weight and bias once, each activation and per-channel
+// parameter once per sample).
 hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
                 const fe::hip::ConvOp* res, const fe::hip::ConvInput& in, fe::hip::View y,
-                fe::hip::View yr, int batch, hipStream_t s) {
+                fe::hip::View yr, int batch, hipStream_t s, fe::hip::SlicePlan slices = {}) {
   if (e.recording) {
     FeEngine::ConvRecord r;
     const char* kind = !in.norm ? "plain" : (in.film_time != nullptr ? "film" : "resid");
@@ -766,6 +786,7 @@ hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
     r.in = in;
     r.y = y;
     r.yr = yr;
+    r.slices = slices;
     const std::uint64_t es = op.bf16 ? 2 : 4;
     r.weight_bytes = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * es + op.oc * 4ull;
     std::uint64_t sb = static_cast<std::uint64_t>(op.ic) * op.lin * 4 +
@@ -785,7 +806,7 @@ hipError_t conv(FeEngine& e, const std::string& site, const fe::hip::ConvOp& op,
     e.conv_records.push_back(std::move(r));
   }
   if (e.dry) return hipSuccess;
-  return dispatch_conv(e, op, res, in, y, yr, batch, s);
+  return dispatch_conv(e, op, res, in, y, yr, batch, s, slices);
 }
 
 // Kernels a convolution runs on at this batch size: the fused weight-streaming kernels (few
@@ -803,11 +824,14 @@ ConvPath conv_path(const FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
   return fused_ok ? ConvPath::kFused : ConvPath::kGeneral;
 }
 
-// Runs one fused convolution on the kernels chosen for this batch size.
+// Runs one fused convolution on the kernels chosen for this batch size.  Sliced convolutions
+// (slices > 1) and inputs made of partial sums run on the fused kernels only.
 hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
                          const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
-                         int batch, hipStream_t s) {
+                         int batch, hipStream_t s, fe::hip::SlicePlan slices) {
   using namespace fe::hip;
+  if (slices.slices > 1 || in.parts > 1 || in.res_parts > 1)
+    return conv_fused(op, res, in, y, yr, batch, s, slices);
   const ConvPath path = conv_path(e, op, res, in, yr, batch);
   if (path == ConvPath::kGeneral) {
     // General shapes: the prologue as its own pass, then the FP32 implicit GEMM.
@@ -853,24 +877,70 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
   return conv_fused(op, res, in, y, yr, batch, s);
 }
 
+// True when this evaluation's convolutions run input-channel sliced.
+bool sliced(const FeEngine& e, int batch) {
+  return e.slice_ok && e.slice_max > 1 && batch >= 1 &&
+         static_cast<std::size_t>(batch) <= e.w.slice_batch &&
+         static_cast<std::size_t>(batch) < e.mfma_batch;
+}
+
+// Input-channel slices of one convolution (1: unsliced), at most `cap`.
+fe::hip::SlicePlan slices_of(const FeEngine& e, const fe::hip::ConvOp& op,
+                             const fe::hip::ConvOp* res, const fe::hip::ConvInput& in, int batch,
+                             int cap = fe::hip::kMaxSlices) {
+  if (!sliced(e, batch)) return {};
+  fe::hip::View yr;
+  yr.p = reinterpret_cast<float*>(e.ws);  // a non-null stand-in: only its presence is checked
+  return fe::hip::conv_fused_slices(op, res, in, yr, batch, std::min(cap, e.slice_max),
+                                    e.slice_tpr);
+}
+
+// Output view of a raw convolution output of `act` floats per sample: with slices, one partial
+// sum per slice, kMaxSlices partials per sample.
+fe::hip::View out_view(float* p, std::int64_t act, int slices) {
+  fe::hip::View v;
+  v.p = p;
+  v.stride = slices > 1 ? act * fe::hip::kMaxSlices : act;
+  v.part = slices > 1 ? act : 0;
+  return v;
+}
+
 // How the current activation tensor is read: a plain tensor, or "virtual" as
-// Y = mish(GroupNorm(src)) + res (a ResidualBlock output that is never stored whole).
+// Y = mish(GroupNorm(src)) + res (a ResidualBlock output that is never stored whole).  `p` and
+// `res` may be sums of partials (outputs of sliced convolutions).
 struct Act {
   bool virt = false;
   const float* p = nullptr;  // plain tensor, or the raw source of a virtual one
   std::int64_t stride = 0;
+  int parts = 1;
+  std::int64_t part_stride = 0;
   const float* gamma = nullptr;
   const float* beta = nullptr;
   const float* res = nullptr;
   std::int64_t res_stride = 0;
+  int res_parts = 1;
+  std::int64_t res_part_stride = 0;
   int channels = 0;
 };
+
+// A plain (non-virtual) activation read from view `v` written by a convolution with `slices`.
+Act plain_act(const fe::hip::View& v, int channels, int slices) {
+  Act a;
+  a.p = v.p;
+  a.stride = v.stride;
+  a.parts = slices;
+  a.part_stride = v.part;
+  a.channels = channels;
+  return a;
+}
 
 fe::hip::ConvInput input_of(const FeEngine& e, const Act& in, float* mat, std::int64_t mat_stride) {
   fe::hip::ConvInput ci;
   ci.src = in.p;
   ci.src_stride = in.stride;
   ci.split = in.channels;
+  ci.parts = in.parts;
+  ci.part_stride = in.part_stride;
   if (in.virt) {
     ci.norm = true;
     ci.gamma = in.gamma;
@@ -878,24 +948,77 @@ fe::hip::ConvInput input_of(const FeEngine& e, const Act& in, float* mat, std::i
     ci.groups = static_cast<int>(e.cfg.groups);
     ci.res = in.res;
     ci.res_stride = in.res_stride;
+    ci.res_parts = in.res_parts;
+    ci.res_part_stride = in.res_part_stride;
     ci.mat = mat;
     ci.mat_stride = mat_stride;
   }
   return ci;
 }
 
+// The FiLM-conditioned conv2 input FiLM(mish(GN1(h1))) of a block whose conv1 wrote view h1.
+fe::hip::ConvInput film_input(const FeEngine& e, const Block& b, const fe::hip::View& h1,
+                              int parts, const float* film_row) {
+  fe::hip::ConvInput c2{};
+  c2.src = h1.p;
+  c2.src_stride = h1.stride;
+  c2.parts = parts;
+  c2.part_stride = h1.part;
+  c2.split = static_cast<int>(b.oc);
+  c2.norm = true;
+  c2.gamma = e.ptr(b.n1.g_off);
+  c2.beta = e.ptr(b.n1.b_off);
+  c2.groups = static_cast<int>(e.cfg.groups);
+  c2.film_time = film_row;
+  c2.film_cond = e.wp(e.w.film_cond);
+  c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
+  c2.film_off = static_cast<int>(b.film_off);
+  return c2;
+}
+
 // One ResidualBlock (diffusion.cc:724-773) as two fused launches:
 //   K1: [conv1 | res 1x1](prologue(input))      -> h1, r
 //   K2: conv2(FiLM(mish(GN1(h1))))               -> h2
-// and returns its output as the virtual Y = mish(GN2(h2)) + (identity ? input : r).
-hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, const Act& in,
-                         int batch, const float* film_row, float* skip_mat,
-                         std::int64_t skip_stride, Act& out) {
+// and returns its output as the virtual Y = mish(GN2(h2)) + (identity ? input : r).  `ci` is
+// the block's input descriptor (input_of, possibly with a plain second part).
+hipError_t enqueue_block_in(FeEngine& e, const std::string& site, const Block& b, const Act& in,
+                            const fe::hip::ConvInput& ci, int batch, const float* film_row,
+                            Act& out) {
   using namespace fe::hip;
   hipStream_t s = e.stream;
   const std::int64_t act = static_cast<std::int64_t>(b.oc * b.len);
-  float* h1 = e.wp(e.w.h1[b.id]);
-  float* h2 = e.wp(e.w.h2[b.id]);
+  const ConvOp* res = b.identity ? nullptr : &b.res.op;
+  const SlicePlan s1 = slices_of(e, b.c1.op, res, ci, batch);
+  const View v1 = out_view(e.wp(e.w.h1[b.id]), act, s1.slices);
+  const View vr = b.identity ? View{} : out_view(e.wp(e.w.r[b.id]), act, s1.slices);
+  FE_TRY(conv(e, site + ".conv1", b.c1.op, res, ci, v1, vr, batch, s, s1));
+  const ConvInput c2 = film_input(e, b, v1, s1.slices, film_row);
+  const SlicePlan s2 = slices_of(e, b.c2.op, nullptr, c2, batch);
+  const View v2 = out_view(e.wp(e.w.h2[b.id]), act, s2.slices);
+  FE_TRY(conv(e, site + ".conv2", b.c2.op, nullptr, c2, v2, View{}, batch, s, s2));
+  out = plain_act(v2, static_cast<int>(b.oc), s2.slices);
+  out.virt = true;
+  out.gamma = e.ptr(b.n2.g_off);
+  out.beta = e.ptr(b.n2.b_off);
+  if (b.identity) {
+    // The identity residual is the block input: the copy conv1's prologue materialised, or the
+    // plain input itself.
+    out.res = in.virt ? ci.mat : in.p;
+    out.res_stride = in.virt ? ci.mat_stride : in.stride;
+    out.res_parts = in.virt ? 1 : in.parts;
+    out.res_part_stride = in.virt ? 0 : in.part_stride;
+  } else {
+    out.res = vr.p;
+    out.res_stride = vr.stride;
+    out.res_parts = s1.slices;
+    out.res_part_stride = vr.part;
+  }
+  return hipSuccess;
+}
+
+hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, const Act& in,
+                         int batch, const float* film_row, float* skip_mat,
+                         std::int64_t skip_stride, Act& out) {
   // Where the (virtual) input is materialised, when something reads it again.
   float* mat = nullptr;
   std::int64_t mat_stride = 0;
@@ -908,38 +1031,7 @@ hipError_t enqueue_block(FeEngine& e, const std::string& site, const Block& b, c
       mat_stride = static_cast<std::int64_t>(b.ic * b.len);
     }
   }
-  ConvInput ci = input_of(e, in, mat, mat_stride);
-  float* r = b.identity ? nullptr : e.wp(e.w.r[b.id]);
-  FE_TRY(conv(e, site + ".conv1", b.c1.op, b.identity ? nullptr : &b.res.op, ci, View{h1, act},
-              View{r, act}, batch, s));
-  ConvInput c2{};
-  c2.src = h1;
-  c2.src_stride = act;
-  c2.split = static_cast<int>(b.oc);
-  c2.norm = true;
-  c2.gamma = e.ptr(b.n1.g_off);
-  c2.beta = e.ptr(b.n1.b_off);
-  c2.groups = static_cast<int>(e.cfg.groups);
-  c2.film_time = film_row;
-  c2.film_cond = e.wp(e.w.film_cond);
-  c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
-  c2.film_off = static_cast<int>(b.film_off);
-  FE_TRY(conv(e, site + ".conv2", b.c2.op, nullptr, c2, View{h2, act}, View{}, batch, s));
-  out = Act{};
-  out.virt = true;
-  out.p = h2;
-  out.stride = act;
-  out.gamma = e.ptr(b.n2.g_off);
-  out.beta = e.ptr(b.n2.b_off);
-  out.channels = static_cast<int>(b.oc);
-  if (b.identity) {
-    out.res = in.virt ? mat : in.p;
-    out.res_stride = in.virt ? mat_stride : in.stride;
-  } else {
-    out.res = r;
-    out.res_stride = act;
-  }
-  return hipSuccess;
+  return enqueue_block_in(e, site, b, in, input_of(e, in, mat, mat_stride), batch, film_row, out);
 }
 
 // Fields of the final GroupNorm + Mish + 1x1 conv that every update of the engine shares.
@@ -985,13 +1077,11 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
         skip_stride = static_cast<std::int64_t>(e.up[u][0].ic * e.up[u][0].len);
       }
       ConvInput ci = input_of(e, x, skip, skip_stride);
-      float* out = e.wp(e.w.ds_out[st]);
       const std::int64_t os = static_cast<std::int64_t>(d.op.oc) * d.op.lout;
-      FE_TRY(conv(e, stage + ".downsample", d.op, nullptr, ci, View{out, os}, View{}, batch, s));
-      x = Act{};
-      x.p = out;
-      x.stride = os;
-      x.channels = d.op.oc;
+      const SlicePlan sd = slices_of(e, d.op, nullptr, ci, batch);
+      const View out = out_view(e.wp(e.w.ds_out[st]), os, sd.slices);
+      FE_TRY(conv(e, stage + ".downsample", d.op, nullptr, ci, out, View{}, batch, s, sd));
+      x = plain_act(out, d.op.oc, sd.slices);
     }
   }
   // Mid blocks; the first one's prologue materialises the bottom stage output as the skip tensor
@@ -1005,83 +1095,59 @@ hipError_t enqueue_unet(FeEngine& e, int batch, const float* film_row, fe::hip::
     FE_TRY(enqueue_block(e, "mid1", e.mid[1], x, batch, film_row, nullptr, 0, y));
     x = y;
   }
+  Act up_in;  // the previous up stage's upsample output
   for (std::size_t u = 0; u + 1 < c.stages; ++u) {
     const Block& r0 = e.up[u][0];
     const std::int64_t cs = static_cast<std::int64_t>(r0.ic * r0.len);
     const int half = static_cast<int>(r0.ic / 2);
-    // Input [x ; skip]: x is the virtual mid output (u == 0) or the previous upsample output that
-    // was written into the first half of this buffer.
-    Act cat;
-    if (u == 0) {
-      cat = x;
-    } else {
-      cat.p = e.wp(e.w.concat[u]);
-      cat.stride = cs;
-      cat.channels = half;
-    }
-    // enqueue_block's input descriptor covers channels [0, half); the skip half is plain.
-    Act in = cat;
+    // Input [x ; skip]: x is the virtual mid output (u == 0) or the previous upsample output;
+    // the block's input descriptor covers channels [0, half), the skip half is plain.
+    Act in = u == 0 ? x : up_in;
     in.channels = half;
-    {
-      using namespace fe::hip;
-      hipStream_t s2 = e.stream;
-      const std::int64_t act = static_cast<std::int64_t>(r0.oc * r0.len);
-      ConvInput ci = input_of(e, in, nullptr, 0);
-      ci.plain = e.wp(e.w.concat[u]) + half * r0.len;
-      ci.plain_stride = cs;
-      const std::string stage = "up" + std::to_string(u);
-      FE_TRY(conv(e, stage + ".b0.conv1", r0.c1.op, &r0.res.op, ci, View{e.wp(e.w.h1[r0.id]), act},
-                  View{e.wp(e.w.r[r0.id]), act}, batch, s2));
-      ConvInput c2{};
-      c2.src = e.wp(e.w.h1[r0.id]);
-      c2.src_stride = act;
-      c2.split = static_cast<int>(r0.oc);
-      c2.norm = true;
-      c2.gamma = e.ptr(r0.n1.g_off);
-      c2.beta = e.ptr(r0.n1.b_off);
-      c2.groups = static_cast<int>(c.groups);
-      c2.film_time = film_row;
-      c2.film_cond = e.wp(e.w.film_cond);
-      c2.film_cond_stride = static_cast<std::int64_t>(e.film_total);
-      c2.film_off = static_cast<int>(r0.film_off);
-      FE_TRY(conv(e, stage + ".b0.conv2", r0.c2.op, nullptr, c2, View{e.wp(e.w.h2[r0.id]), act},
-                  View{}, batch, s2));
-      y = Act{};
-      y.virt = true;
-      y.p = e.wp(e.w.h2[r0.id]);
-      y.stride = act;
-      y.gamma = e.ptr(r0.n2.g_off);
-      y.beta = e.ptr(r0.n2.b_off);
-      y.res = e.wp(e.w.r[r0.id]);
-      y.res_stride = act;
-      y.channels = static_cast<int>(r0.oc);
-      x = y;
-    }
-    FE_TRY(enqueue_block(e, "up" + std::to_string(u) + ".b1", e.up[u][1], x, batch, film_row,
-                         nullptr, 0, y));
+    ConvInput ci = input_of(e, in, nullptr, 0);
+    ci.plain = e.wp(e.w.concat[u]) + half * r0.len;
+    ci.plain_stride = cs;
+    const std::string stage = "up" + std::to_string(u);
+    FE_TRY(enqueue_block_in(e, stage + ".b0", r0, in, ci, batch, film_row, y));
     x = y;
-    // Upsample1d into the first half of the next up stage's input, or the final conv input.
+    FE_TRY(enqueue_block(e, stage + ".b1", e.up[u][1], x, batch, film_row, nullptr, 0, y));
+    x = y;
+    // Upsample1d into the first half of the next up stage's input, or the final conv input; when
+    // sliced, into its own partial-sum buffer.
     const ConvSlot& up = e.us[u];
+    const bool last = u + 2 >= c.stages;
+    ConvInput ci2 = input_of(e, x, nullptr, 0);
+    const SlicePlan su = slices_of(e, up.op, nullptr, ci2, batch);
     View dst;
-    if (u + 2 < c.stages) {
+    if (su.slices > 1) {
+      dst = out_view(e.wp(e.w.us_out[u]), static_cast<std::int64_t>(up.op.oc) * up.op.lout,
+                     su.slices);
+    } else if (!last) {
       dst.p = e.wp(e.w.concat[u + 1]);
       dst.stride = static_cast<std::int64_t>(e.up[u + 1][0].ic * e.up[u + 1][0].len);
     } else {
       dst.p = e.wp(e.w.final_in);
       dst.stride = static_cast<std::int64_t>(c.dims[0] * c.horizon);
     }
-    ConvInput ci = input_of(e, x, nullptr, 0);
-    FE_TRY(conv(e, "up" + std::to_string(u) + ".upsample", up.op, nullptr, ci, dst, View{}, batch,
-                s));
+    FE_TRY(conv(e, stage + ".upsample", up.op, nullptr, ci2, dst, View{}, batch, s, su));
+    up_in = plain_act(dst, up.op.oc, su.slices);
   }
   const std::int64_t fs = static_cast<std::int64_t>(c.dims[0] * c.horizon);
-  float* fo = e.wp(e.w.fconv_out);
   ConvInput fi{};
-  fi.src = e.wp(e.w.final_in);
-  fi.src_stride = fs;
+  fi.src = up_in.p;
+  fi.src_stride = up_in.stride;
+  fi.parts = up_in.parts;
+  fi.part_stride = up_in.part_stride;
   fi.split = static_cast<int>(c.dims[0]);
-  FE_TRY(conv(e, "final.conv", e.fconv.op, nullptr, fi, View{fo, fs}, View{}, batch, s));
+  // The update sums at most kMaxUpdateParts partials of the final conv output.
+  const SlicePlan sf = slices_of(e, e.fconv.op, nullptr, fi, batch,
+                                 update_max_parts(static_cast<int>(c.dims[0])));
+  const View fo = out_view(e.wp(e.w.fconv_out), fs, sf.slices);
+  FE_TRY(conv(e, "final.conv", e.fconv.op, nullptr, fi, fo, View{}, batch, s, sf));
   update_base(e, upd);
+  upd.hparts = sf.slices;
+  upd.hpart = fo.part;
+  upd.hstride = fo.stride;
   if (e.dry) return hipSuccess;
   return update(upd, batch, s);
 }
@@ -1485,24 +1551,73 @@ int hip_fail(const char* what, hipError_t st) {
   return FE_STATUS_RESOURCE_EXHAUSTED;
 }
 
-// Lists the convolutions of one U-Net evaluation (their arguments at batch 1) the first time a
-// diagnostic asks for them, by walking the U-Net without enqueueing anything.
-int ensure_conv_records(FeEngine* e) {
-  if (!e->conv_records.empty()) return FE_STATUS_OK;
+// Lists the convolutions of one U-Net evaluation (their arguments at batch 1, input-channel
+// sliced when an evaluation at `batch` is) the first time a diagnostic asks for them, by walking
+// the U-Net without enqueueing anything.
+int ensure_conv_records(FeEngine* e, std::size_t batch = 1) {
+  const bool want = sliced(*e, static_cast<int>(batch));
+  if (!e->conv_records.empty() && e->records_sliced == want) return FE_STATUS_OK;
+  e->conv_records.clear();
   using namespace fe::hip;
   UpdateOp u{};
   u.kind = kUpdateDenoise;
   u.out = e->wp(e->w.out_action);
+  const bool saved = e->slice_ok;
+  e->slice_ok = saved && want;
   e->recording = true;
   e->dry = true;
   const hipError_t st = enqueue_unet(*e, 1, e->wp(e->w.film_table), u);
   e->recording = false;
   e->dry = false;
+  e->slice_ok = saved;
+  e->records_sliced = want;
   if (st != hipSuccess) {
     e->conv_records.clear();
     return hip_fail("Diagnostic U-Net walk failed", st);
   }
   return FE_STATUS_OK;
+}
+
+// Input-channel slicing is used when every convolution of the model runs on the fused kernels at
+// the batch sizes below the matrix-core threshold and the update sums the final conv's partials,
+// and not with the persistent tick (which runs the unsliced kernels).
+void decide_slicing(FeEngine& e) {
+  e.slice_ok = false;
+  const char* v = std::getenv("FLOWEDGE_SLICES");
+  if (v != nullptr && *v != '\0') {
+    char* end = nullptr;
+    const long n = std::strtol(v, &end, 10);
+    e.slice_max = (end && *end == '\0' && n >= 1) ? static_cast<int>(std::min<long>(n, fe::hip::kMaxSlices)) : 1;
+  }
+  v = std::getenv("FLOWEDGE_SLICE_TPR");
+  if (v != nullptr && (std::strcmp(v, "16") == 0 || std::strcmp(v, "32") == 0 ||
+                       std::strcmp(v, "64") == 0))
+    e.slice_tpr = std::atoi(v);
+  const char* p = std::getenv("FLOWEDGE_PERSISTENT");
+  if (e.slice_max <= 1 || (p != nullptr && std::strcmp(p, "1") == 0) || e.mfma_batch <= 1) return;
+  const Config& c = e.cfg;
+  if (!fe::hip::update_fused(static_cast<int>(c.dims[0]), static_cast<int>(kFinalNormGroups),
+                             static_cast<int>(c.horizon), static_cast<int>(c.action_dim)))
+    return;
+  if (ensure_conv_records(&e) != FE_STATUS_OK) {
+    clear_error();
+    return;
+  }
+  for (const FeEngine::ConvRecord& r : e.conv_records)
+    if (conv_path(e, r.op, r.has_res ? &r.res : nullptr, r.in, r.yr, 1) != ConvPath::kFused) return;
+  // A sliced walk: every convolution left unsliced must read single tensors (the unsliced
+  // kernels do not sum partials).
+  e.slice_ok = true;
+  if (ensure_conv_records(&e, 1) != FE_STATUS_OK) {
+    clear_error();
+    e.slice_ok = false;
+    return;
+  }
+  for (const FeEngine::ConvRecord& r : e.conv_records)
+    if (r.slices.slices == 1 && (r.in.parts != 1 || r.in.res_parts != 1)) {
+      e.slice_ok = false;
+      return;
+    }
 }
 
 // Validates a sampling request (engine_runtime.cc:446-470 + extensions).
@@ -1973,6 +2088,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     }
   }
   build_chain(*e);
+  decide_slicing(*e);
   return e.release();
 }
 
@@ -2607,7 +2723,7 @@ int fe_engine_conv_path(fe_engine* engine, size_t index, size_t batch, int* path
     set_error("Invalid arguments to fe_engine_conv_path");
     return FE_STATUS_INVALID_ARGUMENT;
   }
-  const int rc = ensure_conv_records(engine);
+  const int rc = ensure_conv_records(engine, batch);
   if (rc != FE_STATUS_OK) return rc;
   if (index >= engine->conv_records.size()) {
     set_error("Convolution index out of range");
@@ -2616,6 +2732,22 @@ int fe_engine_conv_path(fe_engine* engine, size_t index, size_t batch, int* path
   const FeEngine::ConvRecord& r = engine->conv_records[index];
   *path = static_cast<int>(conv_path(*engine, r.op, r.has_res ? &r.res : nullptr, r.in, r.yr,
                                      static_cast<int>(batch)));
+  return FE_STATUS_OK;
+}
+
+int fe_engine_conv_slices(fe_engine* engine, size_t index, size_t batch, int* slices) {
+  clear_error();
+  if (engine == nullptr || slices == nullptr || batch == 0 || batch > engine->max_batch) {
+    set_error("Invalid arguments to fe_engine_conv_slices");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  const int rc = ensure_conv_records(engine, batch);
+  if (rc != FE_STATUS_OK) return rc;
+  if (index >= engine->conv_records.size()) {
+    set_error("Convolution index out of range");
+    return FE_STATUS_INVALID_ARGUMENT;
+  }
+  *slices = engine->conv_records[index].slices.slices;
   return FE_STATUS_OK;
 }
 
@@ -2628,7 +2760,7 @@ int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, siz
     return FE_STATUS_INVALID_ARGUMENT;
   }
   FeEngine* e = engine;
-  const int rc = ensure_conv_records(e);
+  const int rc = ensure_conv_records(e, batch);
   if (rc != FE_STATUS_OK) return rc;
   for (size_t i = 0; i < n; ++i)
     if (indices[i] >= e->conv_records.size()) {
@@ -2642,7 +2774,7 @@ int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, siz
     for (size_t i = 0; i < n; ++i) {
       const FeEngine::ConvRecord& r = e->conv_records[indices[i]];
       const hipError_t s2 = dispatch_conv(*e, r.op, r.has_res ? &r.res : nullptr, r.in, r.y,
-                                          r.yr, b, e->stream);
+                                          r.yr, b, e->stream, r.slices);
       if (s2 != hipSuccess) return s2;
     }
     return hipSuccess;

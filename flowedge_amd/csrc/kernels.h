@@ -37,7 +37,16 @@ struct ConvOp {
 struct View {
   float* p = nullptr;
   std::int64_t stride = 0;  // floats between samples
+  std::int64_t part = 0;    // floats between the partial sums of a sliced convolution's output
 };
+
+// Input-channel slices: a fused convolution may split its input channels into up to
+// kMaxSlices slices (whole GroupNorm groups each), one slice per workgroup, and then writes one
+// partial sum per slice ([B][S][oc][lout] at View::part spacing, bias in partial 0); the consumer
+// adds the partials in slice order while it reads them.
+constexpr int kMaxSlices = 8;
+// Staged floats of one slice (channels * positions): one 16-byte chunk per lane.
+constexpr int kSliceFloats = 2048;
 
 // Input of a fused convolution.  Channels [0, split) come from `src` (a raw producer output,
 // bias included) through the optional prologue
@@ -65,16 +74,35 @@ struct ConvInput {
   std::int64_t mat_stride = 0;
   const float* plain = nullptr;
   std::int64_t plain_stride = 0;
+  // `src` and `res` as sums of partials (outputs of sliced convolutions): value = sum over
+  // p < parts of src[p * part_stride + ...], added in order p = 0, 1, ...
+  int parts = 1;
+  std::int64_t part_stride = 0;
+  int res_parts = 1;
+  std::int64_t res_part_stride = 0;
 };
 
 // y = conv(input) + bias, and optionally yr = res1x1(input) + bias from the same prologue (the
 // residual 1x1 projection of a ResidualBlock reads the same input as its first conv).
-hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
-                      View yr, int batch, hipStream_t stream);
+// Input-channel slices of a fused convolution and the lanes per output row of its sliced kernel.
+struct SlicePlan {
+  int slices = 1;
+  int tpr = 0;
+};
 
-// True when conv_fused has a kernel for this convolution, input and batch.
+// With sp.slices > 1 (from conv_fused_slices) the input channels are split into that many
+// slices and y (and yr) receive one partial sum per slice at View::part spacing.
+hipError_t conv_fused(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View y,
+                      View yr, int batch, hipStream_t stream, SlicePlan sp = SlicePlan{});
+
+// True when conv_fused has a kernel for this convolution, input and batch (unsliced).
 bool conv_fused_supported(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr,
                           int batch);
+// The most input-channel slices (a power of two up to max_slices) the sliced kernels can run
+// this convolution with, and their lanes per row (`tpr` if non-zero, else the choice giving the
+// most workgroups); slices 1 when none fits (then `in` must have single-part src and res).
+SlicePlan conv_fused_slices(const ConvOp& op, const ConvOp* res1x1, const ConvInput& in, View yr,
+                            int batch, int max_slices, int tpr = 0);
 
 // Batched path (matrix cores).  y = conv(x) + bias with x a plain tensor: channels [0, split)
 // from `src`, the rest from `plain`.  ic and split are multiples of 16, or split == ic (narrow
@@ -155,6 +183,9 @@ struct UpdateOp {
   int kind = kUpdateDDIM;
   int c0 = 0, horizon = 0, action_dim = 0;
   const float* h = nullptr;      // [B][c0][H] raw final conv output
+  int hparts = 1;                // h as the sum of hparts partials hpart apart (sliced conv)
+  std::int64_t hpart = 0;
+  std::int64_t hstride = 0;      // floats between samples of h (0: c0 * H)
   const float* gamma = nullptr;  // final GroupNorm (8 groups) applied with Mish before the 1x1
   const float* beta = nullptr;
   int groups = 8;
@@ -179,6 +210,10 @@ struct UpdateOp {
 // up to 16, c0 > 1024, more than 64 actions or 32 groups) run on a general kernel (one wavefront
 // per output value), which accepts any c0 divisible by `groups` (at most 64 groups).
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream);
+// True when update() runs this shape on its fused kernel (the one that sums partials of h).
+bool update_fused(int c0, int groups, int horizon, int action_dim);
+// The most partials of h the fused update kernel sums at final width c0.
+int update_max_parts(int c0);
 
 // action[b][t][a] = (x[b][a][t] + 1) / 2 * (max - min) + min   (or a plain transpose when
 // amin == nullptr).

@@ -157,10 +157,10 @@ __global__ void begin_kernel(const float* noise, float* x, float* xin, int h, in
 }
 
 // Final GroupNorm + Mish + 1x1 conv + sampler update, one workgroup per sample (update_body.h).
-template <int H>
+template <int H, int CPL>
 __global__ __launch_bounds__(upd::kUpdThreads) void update_kernel(UpdateOp op) {
   __shared__ upd::UpdateSmem<H> sm;
-  upd::update_body<H, false>(op, blockIdx.x, gridDim.x, sm);
+  upd::update_body<H, false, CPL>(op, blockIdx.x, gridDim.x, sm);
 }
 
 // Shapes outside update_kernel's instances: one wavefront per output value eps[a][t] (lanes
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kUpdGenThreads) void update_general_kernel(UpdateOp
   const int A = op.action_dim, C = op.c0, H = op.horizon;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   constexpr int kWaves = kUpdGenThreads / kWave;
-  const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
+  const float* hb = op.h + b * (op.hstride != 0 ? op.hstride : static_cast<std::int64_t>(C) * H);
   const int cpg = C / op.groups;
   const int n = cpg * H;
   for (int g = wave; g < op.groups; g += kWaves) {
@@ -269,20 +269,42 @@ bool update_fused_ok(int c0, int groups, int horizon, int action_dim) {
 }
 }  // namespace
 
+int update_max_parts(int c0) {
+  return c0 <= upd::kUpdThreads ? upd::kMaxUpdateParts : upd::kMaxUpdateParts / 2;
+}
+
+bool update_fused(int c0, int groups, int horizon, int action_dim) {
+  return update_fused_ok(c0, groups, horizon, action_dim);
+}
+
 hipError_t update(const UpdateOp& op, int batch, hipStream_t stream) {
   if (batch <= 0 || op.c0 <= 0 || op.groups <= 0 || op.groups > kMaxUpdGenGroups ||
       op.c0 % op.groups != 0 || op.action_dim <= 0 || op.horizon <= 0)
+    return hipErrorInvalidValue;
+  // Partial sums of h (sliced final convolution) only on the fused kernel, up to its maximum.
+  if (op.hparts < 1 || op.hparts > update_max_parts(op.c0) ||
+      (op.hparts > 1 && !update_fused_ok(op.c0, op.groups, op.horizon, op.action_dim)))
     return hipErrorInvalidValue;
   if (!update_fused_ok(op.c0, op.groups, op.horizon, op.action_dim)) {
     hipLaunchKernelGGL(update_general_kernel, dim3(batch), dim3(kUpdGenThreads), 0, stream, op);
     return hipGetLastError();
   }
+  if (op.c0 <= upd::kUpdThreads) {
+    switch (op.horizon) {
+      case 1: hipLaunchKernelGGL((update_kernel<1, 1>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+      case 2: hipLaunchKernelGGL((update_kernel<2, 1>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+      case 4: hipLaunchKernelGGL((update_kernel<4, 1>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+      case 8: hipLaunchKernelGGL((update_kernel<8, 1>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+      default: hipLaunchKernelGGL((update_kernel<16, 1>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    }
+    return hipGetLastError();
+  }
   switch (op.horizon) {
-    case 1: hipLaunchKernelGGL(update_kernel<1>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
-    case 2: hipLaunchKernelGGL(update_kernel<2>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
-    case 4: hipLaunchKernelGGL(update_kernel<4>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
-    case 8: hipLaunchKernelGGL(update_kernel<8>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
-    default: hipLaunchKernelGGL(update_kernel<16>, dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 1: hipLaunchKernelGGL((update_kernel<1, 2>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 2: hipLaunchKernelGGL((update_kernel<2, 2>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 4: hipLaunchKernelGGL((update_kernel<4, 2>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    case 8: hipLaunchKernelGGL((update_kernel<8, 2>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
+    default: hipLaunchKernelGGL((update_kernel<16, 2>), dim3(batch), dim3(upd::kUpdThreads), 0, stream, op); break;
   }
   return hipGetLastError();
 }

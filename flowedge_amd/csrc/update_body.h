@@ -113,6 +113,9 @@ __device__ __forceinline__ void apply_update(const UpdateOp& op, std::int64_t sa
 
 constexpr int kUpdThreads = 512;
 constexpr int kMaxUpdateChannelsPerLane = 2;  // c0 <= 1024
+// Partial sums of a sliced final convolution the update adds: 8 channel-rows of loads per lane
+// (kMaxUpdateParts / CPL partials at CPL channels per lane).
+constexpr int kMaxUpdateParts = 8;
 constexpr int kMaxUpdateGroups = 32;
 constexpr int kMaxActions = 64;
 
@@ -135,10 +138,12 @@ struct UpdateSmem {
 // other workgroups of the same launch and are read device-coherently.
 // `state` (CHAIN): the workgroup's own state slot, x, xin and the four flow stages (`values`
 // floats each), used instead of op.x / op.xin / op.kbuf.
-template <int H, bool CHAIN>
+// CPL: channels per lane (c0 <= 512 * CPL).
+template <int H, bool CHAIN, int CPL = kMaxUpdateChannelsPerLane>
 __device__ __forceinline__ void update_body(const UpdateOp& op, int b, int batch,
                                             UpdateSmem<H>& sm, float* state = nullptr) {
-  constexpr int CPL = kMaxUpdateChannelsPerLane;
+  static_assert(CPL >= 1 && CPL <= kMaxUpdateChannelsPerLane, "channels per lane");
+  constexpr int PM = kMaxUpdateParts / CPL;  // partials summed
   constexpr int AG = UpdateSmem<H>::AG;
   constexpr int V = UpdateSmem<H>::V;
   double* ps = sm.ps;
@@ -150,7 +155,7 @@ __device__ __forceinline__ void update_body(const UpdateOp& op, int b, int batch
   const int A = op.action_dim, C = op.c0;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
-  const float* hb = op.h + static_cast<std::int64_t>(b) * C * H;
+  const float* hb = op.h + b * (op.hstride != 0 ? op.hstride : static_cast<std::int64_t>(C) * H);
 
   // Reads that do not depend on the statistics are issued first, so their latency overlaps the
   // reduction: the output conv's weights for the first action group and the sampler state.
@@ -177,24 +182,49 @@ __device__ __forceinline__ void update_body(const UpdateOp& op, int b, int batch
   for (int i = 0; i < CPL; ++i) {
     const int c = tid + i * kUpdThreads;
     const float* p = hb + static_cast<std::int64_t>(c) * H;
-    if constexpr (H >= 4) {
+    if constexpr (CHAIN) {
+      if constexpr (H >= 4) {
 #pragma unroll
-      for (int t = 0; t < H; t += 4) {
-        float4 v = float4{0, 0, 0, 0};
-        if (c < C) {
-          if constexpr (CHAIN)
-            v = ld4_dev(p + t);
-          else
-            v = *reinterpret_cast<const float4*>(p + t);
+        for (int t = 0; t < H; t += 4) {
+          const float4 v = c < C ? ld4_dev(p + t) : float4{0, 0, 0, 0};
+          hv[i][t] = v.x;
+          hv[i][t + 1] = v.y;
+          hv[i][t + 2] = v.z;
+          hv[i][t + 3] = v.w;
         }
-        hv[i][t] = v.x;
-        hv[i][t + 1] = v.y;
-        hv[i][t + 2] = v.z;
-        hv[i][t + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < H; ++t) hv[i][t] = c < C ? ld_dev(p + t) : 0.0f;
       }
     } else {
+      // Sum of the op.hparts partials, in order, with every load issued before the first add.
+      float pv[PM][H];
 #pragma unroll
-      for (int t = 0; t < H; ++t) hv[i][t] = c < C ? (CHAIN ? ld_dev(p + t) : p[t]) : 0.0f;
+      for (int j = 0; j < PM; ++j) {
+        const float* pj = p + j * op.hpart;
+        const bool on = c < C && j < op.hparts;
+        if constexpr (H >= 4) {
+#pragma unroll
+          for (int t = 0; t < H; t += 4) {
+            const float4 v = on ? *reinterpret_cast<const float4*>(pj + t) : float4{0, 0, 0, 0};
+            pv[j][t] = v.x;
+            pv[j][t + 1] = v.y;
+            pv[j][t + 2] = v.z;
+            pv[j][t + 3] = v.w;
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < H; ++t) pv[j][t] = on ? pj[t] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < H; ++t) {
+        float v = pv[0][t];
+#pragma unroll
+        for (int j = 1; j < PM; ++j)
+          if (j < op.hparts) v += pv[j][t];
+        hv[i][t] = v;
+      }
     }
     double s = 0.0, q = 0.0;
 #pragma unroll

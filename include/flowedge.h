@@ -354,6 +354,12 @@ int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name
  * neither of the others has an instance for). */
 int fe_engine_conv_path(fe_engine* engine, size_t index, size_t batch, int* path);
 
+/* Input-channel slices convolution `index` runs with in a sampling call of `batch` samples (1:
+ * unsliced).  A sliced convolution splits its input channels over workgroups (whole GroupNorm
+ * groups per slice) and leaves one partial sum per slice, which its consumers add while reading
+ * it; FLOWEDGE_SLICES at load caps the count (1 turns slicing off). */
+int fe_engine_conv_slices(fe_engine* engine, size_t index, size_t batch, int* slices);
+
 /* Launches convolutions indices[0..n) round-robin `iters` times at `batch` on the engine's stream,
  * on the kernels a sampling call of that batch uses, and returns the mean device time of one
  * launch in microseconds (hipEvents around the loop, after one untimed round).  Outputs land in

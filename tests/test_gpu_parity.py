@@ -293,6 +293,27 @@ def test_pusht_kernel_paths(pusht):
         assert e.conv_paths(4) == ["fused"] * 29
         assert e.conv_paths(5) == ["matrix"] * 29
         assert e.conv_paths(256) == ["matrix"] * 29
+        # Below the matrix-core threshold every convolution but the first (2 input channels) runs
+        # with its input channels split into 8 slices; the matrix cores run unsliced.
+        assert e.conv_slices(1) == [1] + [8] * 28
+        assert e.conv_slices(4) == [1] + [8] * 28
+        assert e.conv_slices(5) == [1] * 29
+
+
+def test_slicing_off_matches_oracle(pusht, monkeypatch):
+    # FLOWEDGE_SLICES=1 at load runs every convolution unsliced (the kernels the persistent tick
+    # shares); both forms agree with the oracle.
+    spec = ck.SPECS["pusht"]
+    cond, noise = ck.inputs(spec, batch=2)
+    o = oracle.Oracle(pusht, threads=8)
+    want = [o.sample(cond[b], noise[b], 10) for b in range(2)]
+    monkeypatch.setenv("FLOWEDGE_SLICES", "1")
+    with flowedge_amd.Engine(pusht) as e:
+        assert e.conv_slices(1) == [1] * 29
+        got = e.sample_diffusion_batch(cond, noise, steps=10)
+    monkeypatch.delenv("FLOWEDGE_SLICES")
+    for b in range(2):
+        assert maxerr(got[b], want[b]) <= TOL
 
 
 def test_bimanual_bf16(ckpt_dir):

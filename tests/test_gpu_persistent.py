@@ -2,11 +2,12 @@
 
 A persistent tick runs every convolution step of every U-Net evaluation in one launch of one
 workgroup per CU, handing activations over through device-coherent memory; the per-layer path
-replays a graph of one launch per convolution.  Both run the same convolution and update code on
-the same plans, so their actions must agree bit for bit; the per-layer path (the default) is
-itself held to the oracle by test_gpu_parity.py.  Repeated ticks must be bit-identical (a stale
-read in the hand-off would show up as run-to-run differences).  FLOWEDGE_PERSISTENT=1 at load
-selects the persistent tick.
+replays a graph of one launch per convolution.  With input-channel slicing off
+(FLOWEDGE_SLICES=1), the per-layer path runs the same convolution and update code on the same
+plans as the tick kernel, so their actions must agree bit for bit; the per-layer path is itself
+held to the oracle by test_gpu_parity.py.  Repeated ticks must be bit-identical (a stale read in
+the hand-off would show up as run-to-run differences).  FLOWEDGE_PERSISTENT=1 at load selects
+the persistent tick (which runs unsliced).
 """
 
 from __future__ import annotations
@@ -32,7 +33,9 @@ def engines(path, monkeypatch):
     monkeypatch.setenv("FLOWEDGE_PERSISTENT", "1")
     chain = flowedge_amd.Engine(path)
     monkeypatch.delenv("FLOWEDGE_PERSISTENT")
+    monkeypatch.setenv("FLOWEDGE_SLICES", "1")
     layers = flowedge_amd.Engine(path)
+    monkeypatch.delenv("FLOWEDGE_SLICES")
     say(f"persistent: {chain.persistent_tick} ({chain.persistent_tick_reason!r}); "
         f"reference engine: {layers.persistent_tick} ({layers.persistent_tick_reason!r})")
     assert chain.persistent_tick, chain.persistent_tick_reason
