@@ -149,6 +149,7 @@ SlicePlan conv_fused_slices(const ConvOp& op, const ConvOp* res1x1, const ConvIn
       if (n > wgs) {
         wgs = n;
         best.slices = S;
+        best.res_slices = S;
         best.tpr = t;
       }
     }

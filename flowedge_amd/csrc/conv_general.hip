@@ -16,6 +16,7 @@
 // the group, then GroupNorm, Mish, FiLM and the residual in one pass.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "device_common.h"
@@ -215,6 +216,21 @@ hipError_t launch_general(GenArgs a, float* workspace, std::size_t workspace_flo
 // ---------------------------------------------------------------------------------------------
 constexpr int kNgThreads = 256;
 
+// Sum of the `parts` partials of one element (`stride` floats apart), added in order; every
+// load is issued before the first add.
+__device__ __forceinline__ float part_sum(const float* p, int parts, std::int64_t stride) {
+  float v[kMaxSlices];
+#pragma unroll
+  for (int j = 0; j < kMaxSlices; ++j) v[j] = j < parts ? p[j * stride] : 0.0f;
+  float s = v[0];
+#pragma unroll
+  for (int j = 1; j < kMaxSlices; ++j)
+    if (j < parts) s += v[j];
+  return s;
+}
+
+constexpr int kNgRegs = 8;  // region values kept in registers between the two passes
+
 __global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput in, int lin,
                                                                       float* dst,
                                                                       std::int64_t dst_stride) {
@@ -225,9 +241,20 @@ __global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput 
   const std::int64_t base = static_cast<std::int64_t>(g) * n;
   const float* src = in.src + b * in.src_stride + base;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  // Sources made of partial sums (a split K loop's outputs) are added while read; the first
+  // kNgRegs values per lane stay in registers for the second pass.
+  float v[kNgRegs];
   double s = 0.0, q = 0.0;
-  for (int i = tid; i < n; i += kNgThreads) {
-    const double d = static_cast<double>(src[i]);
+#pragma unroll
+  for (int r = 0; r < kNgRegs; ++r) {
+    const int i = tid + r * kNgThreads;
+    v[r] = i < n ? part_sum(src + i, in.parts, in.part_stride) : 0.0f;
+    const double d = static_cast<double>(v[r]);
+    s += d;
+    q += d * d;
+  }
+  for (int i = tid + kNgRegs * kNgThreads; i < n; i += kNgThreads) {
+    const double d = static_cast<double>(part_sum(src + i, in.parts, in.part_stride));
     s += d;
     q += d * d;
   }
@@ -254,13 +281,32 @@ __global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput 
       in.film_time != nullptr ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
   float* out = dst + b * dst_stride + base;
   const float* res = in.res != nullptr ? in.res + b * in.res_stride + base : nullptr;
-  for (int i = tid; i < n; i += kNgThreads) {
+  auto put = [&](int i, float x) {
     const int c = g * cpg + i / lin;
-    float val = mish_fast(fmaf(src[i] - meanf, inv * in.gamma[c], in.beta[c]));
+    float val = mish_fast(fmaf(x - meanf, inv * in.gamma[c], in.beta[c]));
     if (ft != nullptr) val = fmaf(ft[c] + fc[c], val, ft[in.split + c] + fc[in.split + c]);
-    if (res != nullptr) val += res[i];
+    if (res != nullptr) val += part_sum(res + i, in.res_parts, in.res_part_stride);
     out[i] = val;
+  };
+#pragma unroll
+  for (int r = 0; r < kNgRegs; ++r) {
+    const int i = tid + r * kNgThreads;
+    if (i < n) put(i, v[r]);
   }
+  for (int i = tid + kNgRegs * kNgThreads; i < n; i += kNgThreads)
+    put(i, part_sum(src + i, in.parts, in.part_stride));
+}
+
+// dst[b][i] = sum over p of src[b][p][i], added in order.
+__global__ __launch_bounds__(kNgThreads) void sum_parts_kernel(const float* src,
+                                                               std::int64_t src_stride, int parts,
+                                                               std::int64_t part_stride,
+                                                               std::int64_t n, float* dst,
+                                                               std::int64_t dst_stride) {
+  const int b = blockIdx.y;
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * kNgThreads + threadIdx.x; i < n;
+       i += static_cast<std::int64_t>(gridDim.x) * kNgThreads)
+    dst[b * dst_stride + i] = part_sum(src + b * src_stride + i, parts, part_stride);
 }
 
 }  // namespace
@@ -306,6 +352,17 @@ hipError_t conv_general(const ConvOp& op, const float* src, std::int64_t src_str
   if (cols <= 16) return launch_general<16>(a, workspace, workspace_floats, stream);
   if (cols <= 32) return launch_general<32>(a, workspace, workspace_floats, stream);
   return launch_general<64>(a, workspace, workspace_floats, stream);
+}
+
+hipError_t sum_parts(const float* src, std::int64_t src_stride, int parts,
+                     std::int64_t part_stride, std::int64_t n, float* dst,
+                     std::int64_t dst_stride, int batch, hipStream_t stream) {
+  if (batch <= 0 || batch > 65535 || parts < 1 || n <= 0) return hipErrorInvalidValue;
+  const std::int64_t blocks = std::min<std::int64_t>((n + kNgThreads - 1) / kNgThreads, 64);
+  hipLaunchKernelGGL(sum_parts_kernel, dim3(static_cast<unsigned>(blocks), batch),
+                     dim3(kNgThreads), 0, stream, src, src_stride, parts, part_stride, n, dst,
+                     dst_stride);
+  return hipGetLastError();
 }
 
 hipError_t norm_act_general(const ConvInput& in, int lin, float* dst, std::int64_t dst_stride,

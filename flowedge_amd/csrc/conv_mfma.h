@@ -35,7 +35,10 @@ struct MmArgs {
   int oc, ic, batch;
   int mtiles, ntiles;
   int ksplit;   // workgroups sharing one output tile's K range (1: no split)
-  float* part;  // ksplit > 1: partial tiles [ksplit][mtiles * ntiles][64 * NT]
+  float* part;  // ksplit > 1, ypart == 0: partial tiles [ksplit][mtiles * ntiles][64 * NT]
+  // ksplit > 1, ypart > 0: split ks writes its partial sum in the output layout at
+  // y + ks * ypart (bias in split 0), and the consumer adds the partials.
+  std::int64_t ypart;
   // Byte sizes of the weight tensor and the batch of `src` / `plain` (buffer ranges of the BF16
   // kernels; each below 2 GiB).
   unsigned wbytes, srcbytes, plainbytes;

@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   }
 
   // Epilogue: lane holds rows 4 * (lane / 16) + e of each 16x16 tile, column lane % 16.
-  if (a.ksplit > 1) {
+  if (a.ksplit > 1 && a.ypart == 0) {
     float* P = a.part + (static_cast<std::int64_t>(ks) * tiles + tile) * (MT * NT);
 #pragma unroll
     for (int i = 0; i < S::TI; ++i)
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     for (int e = 0; e < 4; ++e) {
       const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
       if (oc >= a.oc) continue;
-      const float bias = a.bias[oc];
+      const float bias = ks == 0 ? a.bias[oc] : 0.0f;
 #pragma unroll
       for (int j = 0; j < S::TJ; ++j) {
         const int col = wc * S::WN + 16 * j + l16;
@@ -267,7 +267,8 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
         col_pos(col, NT, S::LOUT, PAR, bl, t);
         const int b = b0 + bl;
         if (b < a.batch)
-          a.y[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] = acc[i][j][e] + bias;
+          a.y[ks * a.ypart + b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
+              acc[i][j][e] + bias;
       }
     }
 }
@@ -455,12 +456,80 @@ bool conv_mfma_supported(const ConvOp& op, int split) {
   return op.mode == kConvTranspose && op.k == 4;
 }
 
+namespace {
+
+// Tile shape, kernel choice and K split of one matrix-core convolution.  With max_parts >= 2 a
+// split K writes up to max_parts partial sums in the output layout (no workspace, no
+// reduction pass); otherwise partial tiles go to a workspace of workspace_floats.
+struct MmPlan {
+  int tile = kTile64x128;
+  int nt_cols = 128;
+  bool narrow = false, use_bf16 = false;
+  int mtiles = 0, ntiles = 0, ksplit = 1;
+  bool in_output = false;
+  std::uint64_t wb = 0, sb = 0, pb = 0;
+};
+
+MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
+               std::int64_t plain_stride, int batch, std::size_t workspace_floats, bool bf16_mma,
+               bool f32_split, int max_parts) {
+  MmPlan p;
+  p.narrow = op.ic % kKC != 0;
+  p.mtiles = (op.oc + 63) / 64;
+  p.ntiles = (batch + 128 / op.lout - 1) / (128 / op.lout);
+  if (p.narrow || p.mtiles * p.ntiles < 256) {
+    p.tile = kTile64x64;
+    p.ntiles = (batch + 64 / op.lout - 1) / (64 / op.lout);
+  }
+  p.nt_cols = p.tile == kTile64x128 ? 128 : 64;
+  const int tiles = p.mtiles * p.ntiles;
+  // The BF16 kernels address weights and inputs through 32-bit buffer offsets.
+  p.wb = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
+  p.sb = static_cast<std::uint64_t>(batch) * src_stride * 4;
+  p.pb = plain != nullptr ? static_cast<std::uint64_t>(batch) * plain_stride * 4 : 0;
+  const bool ranges_fit = p.wb < (1ull << 31) && p.sb < (1ull << 31) && p.pb < (1ull << 31);
+  p.use_bf16 = (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
+  const int nsteps = p.use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
+  // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
+  // workgroups per CU, so that two K steps of weights stream per CU at a time.
+  if (tiles < 256) {
+    int ks = (512 + tiles - 1) / tiles;
+    if (ks > nsteps) ks = nsteps;
+    if (max_parts >= 2) {
+      if (ks > max_parts) ks = max_parts;
+      if (ks > 1) {
+        p.ksplit = ks;
+        p.in_output = true;
+      }
+    } else if (ks > 1 &&
+               static_cast<std::size_t>(ks) * tiles * 64 * p.nt_cols <= workspace_floats) {
+      p.ksplit = ks;
+    }
+  }
+  return p;
+}
+
+}  // namespace
+
+int conv_mfma_parts(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
+                    std::int64_t plain_stride, int batch, bool bf16_mma, bool f32_split,
+                    int max_parts) {
+  if (!conv_mfma_supported(op, split) || batch <= 0 || max_parts < 2) return 1;
+  return mm_plan(op, split, src_stride, plain, plain_stride, batch, 0, bf16_mma, f32_split,
+                 max_parts)
+      .ksplit;
+}
+
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
                      float* workspace, std::size_t workspace_floats, bool bf16_mma,
-                     bool f32_split, hipStream_t stream) {
+                     bool f32_split, hipStream_t stream, int max_parts) {
   if (!conv_mfma_supported(op, split) || batch <= 0) return hipErrorInvalidValue;
   if (split < op.ic && plain == nullptr) return hipErrorInvalidValue;
+  const MmPlan p = mm_plan(op, split, src_stride, plain, plain_stride, batch,
+                           workspace != nullptr ? workspace_floats : 0, bf16_mma, f32_split,
+                           max_parts);
+  if (p.in_output && y.part <= 0) return hipErrorInvalidValue;
   MmArgs a{};
   a.w = op.w;
   a.bias = op.b;
@@ -474,50 +543,28 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
   a.oc = op.oc;
   a.ic = op.ic;
   a.batch = batch;
-  const bool narrow = op.ic % kKC != 0;
-  a.mtiles = (op.oc + 63) / 64;
-  int tile = kTile64x128;
-  a.ntiles = (batch + 128 / op.lout - 1) / (128 / op.lout);
-  if (narrow || a.mtiles * a.ntiles < 256) {
-    tile = kTile64x64;
-    a.ntiles = (batch + 64 / op.lout - 1) / (64 / op.lout);
-  }
-  // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
-  // workgroups per CU, so that two K steps of weights stream per CU at a time.
-  const int nt_cols = tile == kTile64x128 ? 128 : 64;
-  const int tiles = a.mtiles * a.ntiles;
-  // The BF16 kernels address weights and inputs through 32-bit buffer offsets.
-  const std::uint64_t wb = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
-  const std::uint64_t sb = static_cast<std::uint64_t>(batch) * src_stride * 4;
-  const std::uint64_t pb =
-      plain != nullptr ? static_cast<std::uint64_t>(batch) * plain_stride * 4 : 0;
-  const bool ranges_fit = wb < (1ull << 31) && sb < (1ull << 31) && pb < (1ull << 31);
-  const bool use_bf16 =
-      (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
+  a.mtiles = p.mtiles;
+  a.ntiles = p.ntiles;
   // The kernels order ConvTranspose tile columns by output parity (the split-K reduction reads
   // the partial tiles in the same order).
   a.par = op.mode == kConvTranspose ? 1 : 0;
-  a.wbytes = static_cast<unsigned>(wb);
-  a.srcbytes = static_cast<unsigned>(sb);
-  a.plainbytes = static_cast<unsigned>(pb);
-  const int nsteps = use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
-  a.ksplit = 1;
-  if (tiles < 256 && workspace != nullptr) {
-    int ks = (512 + tiles - 1) / tiles;
-    if (ks > nsteps) ks = nsteps;
-    const std::size_t need = static_cast<std::size_t>(ks) * tiles * 64 * nt_cols;
-    if (ks > 1 && need <= workspace_floats) {
-      a.ksplit = ks;
+  a.wbytes = static_cast<unsigned>(p.wb);
+  a.srcbytes = static_cast<unsigned>(p.sb);
+  a.plainbytes = static_cast<unsigned>(p.pb);
+  a.ksplit = p.ksplit;
+  if (p.ksplit > 1) {
+    if (p.in_output)
+      a.ypart = y.part;
+    else
       a.part = workspace;
-    }
   }
-  const hipError_t st = use_bf16  ? launch_mm_bf16(op, tile, a, stream)
-                        : op.bf16 ? by_kernel_mm<true>(op, tile, narrow, a, stream)
-                                  : by_kernel_mm<false>(op, tile, narrow, a, stream);
-  if (st != hipSuccess || a.ksplit == 1) return st;
-  const std::int64_t elems = static_cast<std::int64_t>(tiles) * 64 * nt_cols;
+  const hipError_t st = p.use_bf16 ? launch_mm_bf16(op, p.tile, a, stream)
+                        : op.bf16  ? by_kernel_mm<true>(op, p.tile, p.narrow, a, stream)
+                                   : by_kernel_mm<false>(op, p.tile, p.narrow, a, stream);
+  if (st != hipSuccess || a.ksplit == 1 || p.in_output) return st;
+  const std::int64_t elems = static_cast<std::int64_t>(p.mtiles * p.ntiles) * 64 * p.nt_cols;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((elems + kMmThreads - 1) / kMmThreads)),
-                     dim3(kMmThreads), 0, stream, a, nt_cols, op.lout);
+                     dim3(kMmThreads), 0, stream, a, p.nt_cols, op.lout);
   return hipGetLastError();
 }
 
@@ -526,8 +573,9 @@ hipError_t norm_act(const ConvInput& in, int lin, float* dst, std::int64_t dst_s
   if (!in.norm || batch <= 0 || in.groups <= 0 || in.split % in.groups != 0)
     return hipErrorInvalidValue;
   // Below 256 samples the one-workgroup-per-sample kernel leaves CUs idle; the general form
-  // spreads each sample over one workgroup per group (measured equal at 256).
-  if (batch < 256 || in.groups > 32 || (in.split / in.groups * lin) % 4 != 0 ||
+  // spreads each sample over one workgroup per group (measured equal at 256).  Inputs made of
+  // partial sums run on the general form too.
+  if (batch < 256 || in.parts > 1 || in.res_parts > 1 || in.groups > 32 || (in.split / in.groups * lin) % 4 != 0 ||
       static_cast<std::int64_t>(in.split) * lin > kNaMaxFloats)
     return norm_act_general(in, lin, dst, dst_stride, batch, stream);
   switch (lin) {

@@ -315,7 +315,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   }
 
   // Epilogue: lane holds rows 4 * (lane / 16) + e of each 16x16 tile, column lane % 16.
-  if (a.ksplit > 1) {
+  if (a.ksplit > 1 && a.ypart == 0) {
     float* P = a.part + (static_cast<std::int64_t>(ks) * tiles + tile) * (MT * NT);
 #pragma unroll
     for (int i = 0; i < S::TI; ++i)
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     for (int e = 0; e < 4; ++e) {
       const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
       if (oc >= a.oc) continue;
-      const float bias = a.bias[oc];
+      const float bias = ks == 0 ? a.bias[oc] : 0.0f;
 #pragma unroll
       for (int j = 0; j < S::TJ; ++j) {
         const int col = wc * S::WN + 16 * j + l16;
@@ -340,7 +340,8 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
         col_pos(col, NT, S::LOUT, PAR, bl2, t);
         const int b = b0 + bl2;
         if (b < a.batch)
-          a.y[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] = acc[i][j][e] + bias;
+          a.y[ks * a.ypart + b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
+              acc[i][j][e] + bias;
       }
     }
 }

@@ -58,6 +58,10 @@ constexpr std::size_t kSplitKFloats = 1024 * 64 * 128;  // split-K partials: <= 
 // Largest batch whose convolutions run input-channel sliced (on the fused kernels; the matrix
 // cores take over from 5 samples with F32 weights, 8 with BF16 weights).
 constexpr std::size_t kSliceBatch = 8;
+// Largest batch whose matrix-core convolutions leave the partial sums of a split K loop in the
+// output tensor for their consumers to add (larger batches split K rarely; those that do reduce
+// through the split-K workspace).
+constexpr std::size_t kPartBatch = 64;
 constexpr std::size_t kFinalNormGroups = 8;  // diffusion.cc:28
 constexpr std::size_t kAlign = 256;
 
@@ -199,8 +203,9 @@ struct Work {
   std::size_t ds_out[kMaxStages] = {};  // downsample outputs [B][C][len/2]
   std::size_t us_out[kMaxStages] = {};  // sliced upsample outputs (partials) [B][S][C][2 len]
   // Raw convolution outputs (h1, h2, r, ds_out, us_out, fconv_out) hold, for batches up to
-  // slice_batch, kMaxSlices partial sums per sample ([B][kMaxSlices][C][L]).
-  std::size_t slice_batch = 0;
+  // slice_batch (fused kernels) and part_batch (matrix cores), kMaxSlices partial sums per
+  // sample ([B][kMaxSlices][C][L]).
+  std::size_t slice_batch = 0, part_batch = 0;
   std::size_t h1[kMaxBlocks] = {}, h2[kMaxBlocks] = {};  // raw conv outputs [B][oc][len]
   std::size_t r[kMaxBlocks] = {};     // residual projection [B][oc][len] (non-identity blocks)
   std::size_t xmat[kMaxBlocks] = {};  // materialised block input [B][ic][len] (identity blocks)
@@ -281,9 +286,14 @@ struct FeEngine {
   // slice_batch): on when every convolution of the model runs fused and the final update sums
   // partials; slice_max (FLOWEDGE_SLICES, default kMaxSlices; 1 turns slicing off) caps it.
   bool slice_ok = false;
+  // Matrix-core convolutions leave split-K partial sums for their consumers (batches from
+  // mfma_batch up to the Work's part_batch): on when every convolution runs on the matrix cores
+  // there and the update sums partials; FLOWEDGE_MM_PARTS=0 turns it off.
+  bool mm_parts_ok = false;
   int slice_max = fe::hip::kMaxSlices;
   int slice_tpr = 0;  // lanes per row of the sliced kernels (FLOWEDGE_SLICE_TPR; 0: per shape)
-  bool records_sliced = false;  // conv_records were listed with slicing
+  std::size_t records_batch = 0;  // batch conv_records were listed for (0: none)
+  int records_mode = -1;          // and their partial-sum mode (0 none, 1 sliced, 2 matrix)
   bool bf16_mma = true;        // BF16 weights on the BF16 matrix cores (split input)
   bool f32_split = false;      // F32 weights on the BF16 matrix cores (split weights and input)
 
@@ -575,7 +585,10 @@ Work plan_work(const FeEngine& e, std::size_t batch, std::size_t rows, std::size
     w.concat[u] = plan.take(B * r0.ic * r0.len * 4);
   }
   w.slice_batch = std::min(B, kSliceBatch);
-  const std::size_t PB = std::max(B, static_cast<std::size_t>(fe::hip::kMaxSlices) * w.slice_batch);
+  w.part_batch = std::min(B, kPartBatch);
+  const std::size_t PB =
+      std::max(B, static_cast<std::size_t>(fe::hip::kMaxSlices) *
+                      std::max(w.slice_batch, w.part_batch));
   auto acts = [&](const Block& blk) {
     w.h1[blk.id] = plan.take(PB * blk.oc * blk.len * 4);
     w.h2[blk.id] = plan.take(PB * blk.oc * blk.len * 4);
@@ -825,14 +838,17 @@ ConvPath conv_path(const FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
 }
 
 // Runs one fused convolution on the kernels chosen for this batch size.  Sliced convolutions
-// (slices > 1) and inputs made of partial sums run on the fused kernels only.
+// run on the fused kernels; matrix-core convolutions may leave split-K partial sums (`slices`,
+// planned by plan_of) and add those of their input in the GroupNorm pass (or a summing pass for
+// plain inputs); the general kernels read single tensors.
 hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::ConvOp* res,
                          const fe::hip::ConvInput& in, fe::hip::View y, fe::hip::View yr,
                          int batch, hipStream_t s, fe::hip::SlicePlan slices) {
   using namespace fe::hip;
-  if (slices.slices > 1 || in.parts > 1 || in.res_parts > 1)
+  if (!slices.matrix && (slices.slices > 1 || in.parts > 1 || in.res_parts > 1))
     return conv_fused(op, res, in, y, yr, batch, s, slices);
   const ConvPath path = conv_path(e, op, res, in, yr, batch);
+  if (path == ConvPath::kGeneral && (in.parts > 1 || in.res_parts > 1)) return hipErrorInvalidValue;
   if (path == ConvPath::kGeneral) {
     // General shapes: the prologue as its own pass, then the FP32 implicit GEMM.
     const float* src = in.src;
@@ -854,7 +870,8 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     return hipSuccess;
   }
   if (path == ConvPath::kMatrix) {
-    // Many samples: the prologue as its own pass, then implicit GEMMs on the matrix cores.
+    // Many samples: the prologue as its own pass (adding the producer's partial sums), then
+    // implicit GEMMs on the matrix cores.
     const float* src = in.src;
     std::int64_t ss = in.src_stride;
     if (in.norm) {
@@ -864,14 +881,20 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
       FE_TRY(norm_act(in, op.lin, dst, ds, batch, s));
       src = dst;
       ss = ds;
+    } else if (in.parts > 1) {
+      const std::int64_t n = static_cast<std::int64_t>(in.split) * op.lin;
+      FE_TRY(sum_parts(in.src, in.src_stride, in.parts, in.part_stride, n, e.wp(e.w.xnorm), n,
+                       batch, s));
+      src = e.wp(e.w.xnorm);
+      ss = n;
     }
     float* ws = e.wp(e.w.splitk);
     const std::size_t wsf = e.w.splitk_floats;
     FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws, wsf,
-                     e.bf16_mma, e.f32_split, s));
+                     e.bf16_mma, e.f32_split, s, slices.matrix ? slices.slices : 0));
     if (res != nullptr)
       FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws, wsf,
-                       e.bf16_mma, e.f32_split, s));
+                       e.bf16_mma, e.f32_split, s, slices.matrix ? slices.res_slices : 0));
     return hipSuccess;
   }
   return conv_fused(op, res, in, y, yr, batch, s);
@@ -884,15 +907,37 @@ bool sliced(const FeEngine& e, int batch) {
          static_cast<std::size_t>(batch) < e.mfma_batch;
 }
 
-// Input-channel slices of one convolution (1: unsliced), at most `cap`.
+// True when this evaluation's matrix-core convolutions leave split-K partial sums.
+bool mm_parts(const FeEngine& e, int batch) {
+  return e.mm_parts_ok && batch >= 1 && static_cast<std::size_t>(batch) >= e.mfma_batch &&
+         static_cast<std::size_t>(batch) <= e.w.part_batch;
+}
+
+// Partial sums of one convolution's output (1: a single tensor), at most `cap`: input-channel
+// slices on the fused kernels, or the split K loop of a matrix-core convolution.
 fe::hip::SlicePlan slices_of(const FeEngine& e, const fe::hip::ConvOp& op,
                              const fe::hip::ConvOp* res, const fe::hip::ConvInput& in, int batch,
                              int cap = fe::hip::kMaxSlices) {
-  if (!sliced(e, batch)) return {};
   fe::hip::View yr;
   yr.p = reinterpret_cast<float*>(e.ws);  // a non-null stand-in: only its presence is checked
-  return fe::hip::conv_fused_slices(op, res, in, yr, batch, std::min(cap, e.slice_max),
-                                    e.slice_tpr);
+  if (sliced(e, batch))
+    return fe::hip::conv_fused_slices(op, res, in, yr, batch, std::min(cap, e.slice_max),
+                                      e.slice_tpr);
+  fe::hip::SlicePlan p;
+  if (!mm_parts(e, batch) || conv_path(e, op, res, in, yr, batch) != ConvPath::kMatrix) return p;
+  // The GEMM reads the prologue's output (or the summed plain input) when there is one.
+  const bool staged = in.norm || in.parts > 1;
+  const std::int64_t ss =
+      staged ? (in.norm && in.mat != nullptr ? in.mat_stride
+                                             : static_cast<std::int64_t>(in.split) * op.lin)
+             : in.src_stride;
+  p.matrix = true;
+  p.slices = fe::hip::conv_mfma_parts(op, in.split, ss, in.plain, in.plain_stride, batch,
+                                      e.bf16_mma, e.f32_split, cap);
+  if (res != nullptr)
+    p.res_slices = fe::hip::conv_mfma_parts(*res, in.split, ss, in.plain, in.plain_stride, batch,
+                                            e.bf16_mma, e.f32_split, cap);
+  return p;
 }
 
 // Output view of a raw convolution output of `act` floats per sample: with slices, one partial
@@ -990,7 +1035,7 @@ hipError_t enqueue_block_in(FeEngine& e, const std::string& site, const Block& b
   const ConvOp* res = b.identity ? nullptr : &b.res.op;
   const SlicePlan s1 = slices_of(e, b.c1.op, res, ci, batch);
   const View v1 = out_view(e.wp(e.w.h1[b.id]), act, s1.slices);
-  const View vr = b.identity ? View{} : out_view(e.wp(e.w.r[b.id]), act, s1.slices);
+  const View vr = b.identity ? View{} : out_view(e.wp(e.w.r[b.id]), act, s1.res_slices);
   FE_TRY(conv(e, site + ".conv1", b.c1.op, res, ci, v1, vr, batch, s, s1));
   const ConvInput c2 = film_input(e, b, v1, s1.slices, film_row);
   const SlicePlan s2 = slices_of(e, b.c2.op, nullptr, c2, batch);
@@ -1010,7 +1055,7 @@ hipError_t enqueue_block_in(FeEngine& e, const std::string& site, const Block& b
   } else {
     out.res = vr.p;
     out.res_stride = vr.stride;
-    out.res_parts = s1.slices;
+    out.res_parts = s1.res_slices;
     out.res_part_stride = vr.part;
   }
   return hipSuccess;
@@ -1551,38 +1596,55 @@ int hip_fail(const char* what, hipError_t st) {
   return FE_STATUS_RESOURCE_EXHAUSTED;
 }
 
-// Lists the convolutions of one U-Net evaluation (their arguments at batch 1, input-channel
-// sliced when an evaluation at `batch` is) the first time a diagnostic asks for them, by walking
-// the U-Net without enqueueing anything.
+// Partial-sum mode of an evaluation of `batch` samples: 0 single tensors, 1 input-channel sliced
+// fused kernels, 2 matrix-core split-K partials.
+int parts_mode(const FeEngine& e, int batch) {
+  return sliced(e, batch) ? 1 : (mm_parts(e, batch) ? 2 : 0);
+}
+
+// Lists the convolutions of one U-Net evaluation the first time a diagnostic asks for them, by
+// walking the U-Net without enqueueing anything, with the arguments an evaluation of `batch`
+// samples uses (they depend on the batch only through the partial-sum plan: the listing is
+// taken at batch 1 unless matrix-core partials are on).
 int ensure_conv_records(FeEngine* e, std::size_t batch = 1) {
-  const bool want = sliced(*e, static_cast<int>(batch));
-  if (!e->conv_records.empty() && e->records_sliced == want) return FE_STATUS_OK;
+  const int mode = parts_mode(*e, static_cast<int>(batch));
+  const std::size_t walk = mode == 2 ? batch : 1;
+  if (!e->conv_records.empty() && e->records_mode == mode && e->records_batch == walk)
+    return FE_STATUS_OK;
   e->conv_records.clear();
   using namespace fe::hip;
   UpdateOp u{};
   u.kind = kUpdateDenoise;
   u.out = e->wp(e->w.out_action);
-  const bool saved = e->slice_ok;
-  e->slice_ok = saved && want;
+  const bool saved_slice = e->slice_ok, saved_mm = e->mm_parts_ok;
+  e->slice_ok = saved_slice && mode == 1;
+  e->mm_parts_ok = saved_mm && mode == 2;
   e->recording = true;
   e->dry = true;
-  const hipError_t st = enqueue_unet(*e, 1, e->wp(e->w.film_table), u);
+  const hipError_t st = enqueue_unet(*e, static_cast<int>(walk), e->wp(e->w.film_table), u);
   e->recording = false;
   e->dry = false;
-  e->slice_ok = saved;
-  e->records_sliced = want;
+  e->slice_ok = saved_slice;
+  e->mm_parts_ok = saved_mm;
+  e->records_mode = mode;
+  e->records_batch = walk;
   if (st != hipSuccess) {
     e->conv_records.clear();
+    e->records_mode = -1;
     return hip_fail("Diagnostic U-Net walk failed", st);
   }
   return FE_STATUS_OK;
 }
 
-// Input-channel slicing is used when every convolution of the model runs on the fused kernels at
-// the batch sizes below the matrix-core threshold and the update sums the final conv's partials,
-// and not with the persistent tick (which runs the unsliced kernels).
-void decide_slicing(FeEngine& e) {
+// Partial sums instead of whole tensors between convolutions:
+//  - input-channel slicing, when every convolution of the model runs on the fused kernels below
+//    the matrix-core threshold (and not with the persistent tick, which runs unsliced kernels);
+//  - matrix-core split-K partials, when every convolution runs on the matrix cores from the
+//    threshold on;
+// both only when the update is the fused instance that sums partials of the final conv.
+void decide_partials(FeEngine& e) {
   e.slice_ok = false;
+  e.mm_parts_ok = false;
   const char* v = std::getenv("FLOWEDGE_SLICES");
   if (v != nullptr && *v != '\0') {
     char* end = nullptr;
@@ -1593,8 +1655,10 @@ void decide_slicing(FeEngine& e) {
   if (v != nullptr && (std::strcmp(v, "16") == 0 || std::strcmp(v, "32") == 0 ||
                        std::strcmp(v, "64") == 0))
     e.slice_tpr = std::atoi(v);
+  v = std::getenv("FLOWEDGE_MM_PARTS");
+  const bool mm_wanted = !(v != nullptr && std::strcmp(v, "0") == 0);
   const char* p = std::getenv("FLOWEDGE_PERSISTENT");
-  if (e.slice_max <= 1 || (p != nullptr && std::strcmp(p, "1") == 0) || e.mfma_batch <= 1) return;
+  if (p != nullptr && std::strcmp(p, "1") == 0) return;
   const Config& c = e.cfg;
   if (!fe::hip::update_fused(static_cast<int>(c.dims[0]), static_cast<int>(kFinalNormGroups),
                              static_cast<int>(c.horizon), static_cast<int>(c.action_dim)))
@@ -1603,8 +1667,16 @@ void decide_slicing(FeEngine& e) {
     clear_error();
     return;
   }
-  for (const FeEngine::ConvRecord& r : e.conv_records)
-    if (conv_path(e, r.op, r.has_res ? &r.res : nullptr, r.in, r.yr, 1) != ConvPath::kFused) return;
+  bool fused = e.mfma_batch > 1 && e.slice_max > 1;
+  bool matrix = mm_wanted && e.mfma_batch <= kPartBatch;
+  for (const FeEngine::ConvRecord& r : e.conv_records) {
+    const fe::hip::ConvOp* res = r.has_res ? &r.res : nullptr;
+    fused = fused && conv_path(e, r.op, res, r.in, r.yr, 1) == ConvPath::kFused;
+    matrix = matrix && conv_path(e, r.op, res, r.in, r.yr, static_cast<int>(e.mfma_batch)) ==
+                           ConvPath::kMatrix;
+  }
+  e.mm_parts_ok = matrix;
+  if (!fused) return;
   // A sliced walk: every convolution left unsliced must read single tensors (the unsliced
   // kernels do not sum partials).
   e.slice_ok = true;
@@ -2088,7 +2160,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
     }
   }
   build_chain(*e);
-  decide_slicing(*e);
+  decide_partials(*e);
   return e.release();
 }
 

@@ -88,6 +88,10 @@ struct ConvInput {
 struct SlicePlan {
   int slices = 1;
   int tpr = 0;
+  // Matrix-core convolutions: partial sums left by the split K loop of the convolution and of
+  // its 1x1 projection (1: reduced in place).
+  bool matrix = false;
+  int res_slices = 1;
 };
 
 // With sp.slices > 1 (from conv_fused_slices) the input channels are split into that many
@@ -114,10 +118,21 @@ bool conv_mfma_supported(const ConvOp& op, int split);
 // the input split into two BF16 terms (`bf16_mma`), F32 weights as three products of split
 // weights and split input (`f32_split`).  Otherwise they run on the F32 matrix cores (BF16
 // weights widened).
+// With max_parts >= 2, a split K loop writes up to max_parts partial sums in the output layout
+// (y.part apart, bias in the first) instead of reducing them; conv_mfma_parts returns how many
+// (1: unsplit).
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
                      float* workspace, std::size_t workspace_floats, bool bf16_mma,
-                     bool f32_split, hipStream_t stream);
+                     bool f32_split, hipStream_t stream, int max_parts = 0);
+int conv_mfma_parts(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
+                    std::int64_t plain_stride, int batch, bool bf16_mma, bool f32_split,
+                    int max_parts);
+// dst[b][0 : n) = sum over p < parts of src[b * src_stride + p * part_stride + ...), added in
+// order: the plain input of a matrix-core convolution whose producer left partial sums.
+hipError_t sum_parts(const float* src, std::int64_t src_stride, int parts,
+                     std::int64_t part_stride, std::int64_t n, float* dst,
+                     std::int64_t dst_stride, int batch, hipStream_t stream);
 
 // The prologue of a ConvInput with `norm` on its own: dst[b][0 : split*lin) =
 // mish(GN(src)) [* scale + shift] [+ res], per sample.  Batches under 256 samples and shapes

@@ -354,10 +354,12 @@ int fe_engine_conv_info(fe_engine* engine, size_t index, char* name, size_t name
  * neither of the others has an instance for). */
 int fe_engine_conv_path(fe_engine* engine, size_t index, size_t batch, int* path);
 
-/* Input-channel slices convolution `index` runs with in a sampling call of `batch` samples (1:
- * unsliced).  A sliced convolution splits its input channels over workgroups (whole GroupNorm
- * groups per slice) and leaves one partial sum per slice, which its consumers add while reading
- * it; FLOWEDGE_SLICES at load caps the count (1 turns slicing off). */
+/* Partial sums convolution `index` leaves in a sampling call of `batch` samples (1: a single
+ * tensor).  Below the matrix-core threshold these are input-channel slices: the convolution
+ * splits its input channels over workgroups (whole GroupNorm groups per slice) and leaves one
+ * partial sum per slice (FLOWEDGE_SLICES at load caps the count; 1 turns slicing off).  On the
+ * matrix cores they are the partial sums of a split K loop (FLOWEDGE_MM_PARTS=0: reduced in
+ * place).  Consumers add the partials while reading them. */
 int fe_engine_conv_slices(fe_engine* engine, size_t index, size_t batch, int* slices);
 
 /* Launches convolutions indices[0..n) round-robin `iters` times at `batch` on the engine's stream,
