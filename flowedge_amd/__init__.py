@@ -40,7 +40,9 @@ EXPORTS = [
     "fe_weights_model_digest", "fe_engine_conv_path", "fe_engine_conv_slices",
     "fe_engine_graph_captures",
     "fe_engine_diffusion_denoise_noalloc", "fe_engine_persistent_tick",
-    "fe_engine_persistent_tick_reason",
+    "fe_engine_persistent_tick_reason", "fe_encoder_load", "fe_encoder_free", "fe_encoder_shape",
+    "fe_encoder_encode", "fe_encoder_encode_device", "fe_encoder_last_device_ms",
+    "fe_encoder_device_bytes",
 ]
 
 SCHEDULERS = {"ddim": 0, "ddpm": 1}
@@ -156,6 +158,17 @@ def lib():
     L.fe_engine_diffusion_begin_generation.argtypes = [vp, _f32p, _f32p, sz, cint, u64, u64]
     L.fe_engine_diffusion_advance.argtypes = [vp, sz, _f32p, ctypes.POINTER(sz)]
     L.fe_weights_model_digest.argtypes = [vp, ctypes.POINTER(ctypes.c_uint8 * 16)]
+    L.fe_encoder_load.restype = vp
+    L.fe_encoder_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, sz, sz, sz, sz, sz]
+    L.fe_encoder_free.restype = None
+    L.fe_encoder_free.argtypes = [vp]
+    L.fe_encoder_shape.argtypes = [vp, ctypes.POINTER(sz), ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    L.fe_encoder_encode.argtypes = [vp, _f32p, sz, _f32p]
+    L.fe_encoder_encode_device.argtypes = [vp, vp, sz, vp, sz, sz]
+    L.fe_encoder_last_device_ms.restype = ctypes.c_float
+    L.fe_encoder_last_device_ms.argtypes = [vp]
+    L.fe_encoder_device_bytes.restype = sz
+    L.fe_encoder_device_bytes.argtypes = [vp]
     _lib = L
     return L
 

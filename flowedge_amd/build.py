@@ -22,7 +22,8 @@ SOURCES = ["csrc/engine.cpp", "csrc/safetensors.cpp", "csrc/kernels.hip", "csrc/
            "csrc/conv_slice_s32.hip", "csrc/conv_slice_l32.hip", "csrc/conv_slice_s64.hip",
            "csrc/conv_slice_l64.hip",
            "csrc/conv_mfma.hip", "csrc/conv_mfma_bf16.hip", "csrc/conv_general.hip",
-           "csrc/identity.cpp", "csrc/scratch.hip", "csrc/chain.hip"]
+           "csrc/identity.cpp", "csrc/scratch.hip", "csrc/chain.hip", "csrc/encoder.hip",
+           "csrc/encoder.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=on: a multiply and an add fuse only within one expression, so a kernel body
 # rounds the same way in every kernel it is inlined into (the persistent tick kernel and the

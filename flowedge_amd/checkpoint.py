@@ -302,3 +302,101 @@ def inputs(spec: UNetSpec, batch: int = 1, cond_seed: int = 1, noise_seed: int =
     noise = gaussian(noise_seed, batch * spec.horizon * spec.action_dim).reshape(
         batch, spec.horizon, spec.action_dim)
     return cond, noise
+
+
+# ---- Observation encoder (LeRobot DiffusionRgbEncoder: resnet18 + GroupNorm + SpatialSoftmax) ----
+
+ENCODER_PREFIX = "diffusion.rgb_encoder."
+
+
+@dataclass
+class EncoderSpec:
+    """Shape of a Diffusion Policy RGB encoder: resnet18 widths, crop and keypoints."""
+
+    channels: int = 3
+    image_hw: tuple = (96, 96)   # camera image (pusht)
+    crop_hw: tuple | None = (84, 84)
+    keypoints: int = 32
+    stages: tuple = (64, 128, 256, 512)
+
+    def feature_map_hw(self) -> tuple:
+        h, w = self.crop_hw if self.crop_hw is not None else self.image_hw
+        for _ in range(5):  # stem conv, max pool, stages 2-4: stride 2 each, padding "same"
+            h, w = (h + 1) // 2, (w + 1) // 2
+        return h, w
+
+
+def encoder_layout(spec: EncoderSpec):
+    """Yield ``(name, shape, kind, fan_in)`` of the encoder's state dict (LeRobot names, without
+    the ``diffusion.rgb_encoder.`` prefix).  ``kind``: "w" (weight), "b" (bias), "gw"/"gb"
+    (GroupNorm affine), "grid" (SpatialSoftmax position buffer)."""
+    c0 = spec.stages[0]
+    yield "backbone.0.weight", (c0, spec.channels, 7, 7), "w", spec.channels * 49
+    yield "backbone.1.weight", (c0,), "gw", 0
+    yield "backbone.1.bias", (c0,), "gb", 0
+    cin = c0
+    for s, cout in enumerate(spec.stages):
+        for blk in range(2):
+            p = f"backbone.{4 + s}.{blk}."
+            ic = cin if blk == 0 else cout
+            yield p + "conv1.weight", (cout, ic, 3, 3), "w", ic * 9
+            yield p + "bn1.weight", (cout,), "gw", 0
+            yield p + "bn1.bias", (cout,), "gb", 0
+            yield p + "conv2.weight", (cout, cout, 3, 3), "w", cout * 9
+            yield p + "bn2.weight", (cout,), "gw", 0
+            yield p + "bn2.bias", (cout,), "gb", 0
+            if blk == 0 and s > 0:
+                yield p + "downsample.0.weight", (cout, ic, 1, 1), "w", ic
+                yield p + "downsample.1.weight", (cout,), "gw", 0
+                yield p + "downsample.1.bias", (cout,), "gb", 0
+        cin = cout
+    k = spec.keypoints
+    h, w = spec.feature_map_hw()
+    yield "pool.nets.weight", (k, cin, 1, 1), "w", cin
+    yield "pool.nets.bias", (k,), "b", cin
+    yield "pool.pos_grid", (h * w, 2), "grid", 0
+    yield "out.weight", (2 * k, 2 * k), "w", 2 * k
+    yield "out.bias", (2 * k,), "b", 2 * k
+
+
+def synthetic_encoder_tensors(spec: EncoderSpec, seed: int = 3, prefix: str = ENCODER_PREFIX):
+    """Yield ``(name, float32 array)``: weights and biases U(+-1/sqrt(fan_in)) as PyTorch's
+    default initialisation, GroupNorm affine 1 + U(+-0.1) and U(+-0.1) (so the affine terms are
+    exercised), drawn from one splitmix64 stream in layout order."""
+    cursor = 0
+    for name, shape, kind, fan_in in encoder_layout(spec):
+        count = int(np.prod(shape))
+        if kind == "grid":
+            h, w = spec.feature_map_hw()
+            px, py = np.meshgrid(np.linspace(-1.0, 1.0, w), np.linspace(-1.0, 1.0, h))
+            yield prefix + name, np.stack([px.reshape(-1), py.reshape(-1)], 1).astype(np.float32)
+            continue
+        u = splitmix_uniform(seed, cursor, count).astype(np.float64)
+        cursor += count
+        if kind in ("w", "b"):
+            v = (2.0 * u - 1.0) / np.sqrt(fan_in)
+        elif kind == "gw":
+            v = 1.0 + 0.1 * (2.0 * u - 1.0)
+        else:
+            v = 0.1 * (2.0 * u - 1.0)
+        yield prefix + name, v.astype(np.float32).reshape(shape)
+
+
+def cached_encoder(directory: str | None = None, spec: EncoderSpec | None = None,
+                   seed: int = 3) -> str:
+    """Path of a synthetic encoder checkpoint (LeRobot tensor names), generated once."""
+    spec = spec or EncoderSpec()
+    directory = directory or os.environ.get("FLOWEDGE_CKPT_DIR") or os.path.join(
+        os.environ.get("TMPDIR", "/tmp"), "flowedge_ckpt")
+    os.makedirs(directory, exist_ok=True)
+    tag = f"{spec.image_hw[0]}x{spec.image_hw[1]}_c{spec.channels}_k{spec.keypoints}"
+    path = os.path.join(directory, f"rgb_encoder_{tag}_seed{seed}.safetensors")
+    if not os.path.exists(path):
+        write_safetensors(path, synthetic_encoder_tensors(spec, seed))
+    return path
+
+
+def encoder_images(spec: EncoderSpec, n: int, seed: int = 5) -> np.ndarray:
+    """``n`` normalized images [n][C][H][W] from the seeded Gaussian stream."""
+    h, w = spec.image_hw
+    return gaussian(seed, n * spec.channels * h * w).reshape(n, spec.channels, h, w)

@@ -2873,3 +2873,11 @@ float fe_engine_last_device_ms(const fe_engine* engine) {
 }
 
 }  // extern "C"
+
+// The thread-local error and the allocation counter, for the library's other C ABI translation
+// units (the observation encoder).
+namespace fe::abi {
+void set_error(const std::string& msg) { ::set_error(msg); }
+void clear_error() { ::clear_error(); }
+void count_device_alloc() { g_device_allocs.fetch_add(1); }
+}  // namespace fe::abi

@@ -369,6 +369,37 @@ int fe_engine_conv_slices(fe_engine* engine, size_t index, size_t batch, int* sl
 int fe_engine_time_convs(fe_engine* engine, const size_t* indices, size_t n, size_t batch,
                          size_t iters, float* avg_us);
 
+/* ---- Observation encoder (extension; no counterpart in the reference's C ABI) ----
+ * The Diffusion Policy RGB encoder the reference's LeRobot integration runs through torch
+ * (integrations/lerobot/src/flowedge_lerobot/observation.py:152-216, LeRobot's
+ * DiffusionRgbEncoder): center crop, resnet18 trunk with GroupNorm(C/16), spatial-softmax
+ * keypoints, linear + ReLU.  It maps normalized camera images [n][C][H][W] (float32) to image
+ * features [n][F] (F = 64 for 32 keypoints), the image part of the head's condition, which
+ * stacks [state, image features, environment state] per observation step (observation.py:
+ * 193-216). */
+typedef struct FeEncoder fe_encoder;
+
+/* Loads the encoder tensors named with LeRobot's state-dict names under `prefix`
+ * ("diffusion.rgb_encoder." in a LeRobot model.safetensors) for images of image_height x
+ * image_width, center-cropped to crop_height x crop_width (0 x 0: no crop), and up to max_images
+ * images per call (1-64).  One device allocation at load.  Returns NULL with the error set when
+ * a tensor is missing or its shape breaks the resnet18 structure. */
+fe_encoder* fe_encoder_load(const char* path, const char* prefix, size_t image_height,
+                            size_t image_width, size_t crop_height, size_t crop_width,
+                            size_t max_images);
+void fe_encoder_free(fe_encoder* encoder);
+int fe_encoder_shape(const fe_encoder* encoder, size_t* channels, size_t* feature_dim,
+                     size_t* keypoints);
+/* Host buffers: features[n][F] of images[n][C][H][W]; rejects non-finite pixels. */
+int fe_encoder_encode(fe_encoder* encoder, const float* images, size_t n, float* features);
+/* Device buffers: image i's features go to features_dev + i * out_stride + out_offset (so they
+ * can land inside a condition vector); returns once they are written. */
+int fe_encoder_encode_device(fe_encoder* encoder, const float* images_dev, size_t n,
+                             float* features_dev, size_t out_stride, size_t out_offset);
+/* Device time of the last encode (hipEvents around the encoder graph), milliseconds. */
+float fe_encoder_last_device_ms(const fe_encoder* encoder);
+size_t fe_encoder_device_bytes(const fe_encoder* encoder);
+
 #ifdef __cplusplus
 }
 #endif
