@@ -5,9 +5,9 @@
 // the GPU:
 //   * load: read the encoder tensors (LeRobot names under a prefix, "diffusion.rgb_encoder." in a
 //     LeRobot model.safetensors), check the resnet18 structure, plan ONE device arena for the
-//     repacked weights (convolutions [O][tap][C]) and the activations of `max_images` images,
+//     repacked weights (convolutions step-major over tap * C + channel) and the activations of `max_images` images,
 //     one hipMalloc, uploads;
-//   * encode: one hipGraph replay per image count (captured on first use): 38 launches of
+//   * encode: one hipGraph replay per image count (captured on first use): 40 launches of
 //     encoder.hip's convolution, GroupNorm and head kernels.
 #include <hip/hip_runtime.h>
 
@@ -79,7 +79,9 @@ struct FeEncoder {
   std::size_t nets_w = 0, nets_b = 0, grid = 0, out_w = 0, out_b = 0;
   // Workspace offsets.
   std::size_t images = 0, stem_parts = 0, x0 = 0, x1 = 0, a1 = 0, h1 = 0, h2 = 0, hd = 0;
+  std::size_t stats = 0;  // GroupNorm chunk statistics (doubles)
   std::size_t features = 0;
+  std::size_t kp = 0;       // keypoint coordinates [n][2K]
   std::size_t act_max = 0;  // floats of the largest block activation per image
   std::map<std::size_t, hipGraphExec_t> graphs;
 
@@ -156,7 +158,8 @@ struct Builder {
     return off;
   }
 
-  // A convolution weight [O][C][k][k] repacked to [O][k * k][C].
+  // A convolution weight [O][C][k][k] repacked step-major: [steps][O][kReduceChunk] over the
+  // reduction index tap * C + channel, zero past its end.
   bool conv(const std::string& name, int cin, int cout, int k, int stride, int pad, ConvW& c) {
     const fe::TensorInfo* t = get(name, {static_cast<std::size_t>(cout),
                                          static_cast<std::size_t>(cin),
@@ -164,13 +167,17 @@ struct Builder {
                                          static_cast<std::size_t>(k)});
     if (t == nullptr) return false;
     const std::vector<float> w = widen(t);
-    std::vector<float> r(w.size());
     const int taps = k * k;
+    const int kdim = taps * cin;
+    const int steps = (kdim + enc::kReduceChunk - 1) / enc::kReduceChunk;
+    std::vector<float> r(static_cast<std::size_t>(steps) * cout * enc::kReduceChunk, 0.0f);
     for (int o = 0; o < cout; ++o)
-      for (int ci = 0; ci < cin; ++ci)
-        for (int tap = 0; tap < taps; ++tap)
-          r[(static_cast<std::size_t>(o) * taps + tap) * cin + ci] =
-              w[(static_cast<std::size_t>(o) * cin + ci) * taps + tap];
+      for (int kk = 0; kk < kdim; ++kk) {
+        const int tap = kk / cin, ci = kk % cin;
+        const int s = kk / enc::kReduceChunk, j = kk % enc::kReduceChunk;
+        r[(static_cast<std::size_t>(s) * cout + o) * enc::kReduceChunk + j] =
+            w[(static_cast<std::size_t>(o) * cin + ci) * taps + tap];
+      }
     c.off = plan.take(r.size() * 4);
     c.cin = cin;
     c.cout = cout;
@@ -279,7 +286,7 @@ struct Builder {
     L.feature = static_cast<int>(ow->shape[0]);
     const fe::TensorInfo* ob = get("out.bias", {static_cast<std::size_t>(L.feature)});
     if (ob == nullptr) return false;
-    if (enc::head_lds_bytes(cin, h * w, L.keypoints) > enc::kMaxHeadLds) {
+    if (h * w > enc::kMaxHeadPos || 2 * L.keypoints > enc::kMaxHeadInputs) {
       err = "Encoder feature map too large for the keypoint head";
       return false;
     }
@@ -307,17 +314,55 @@ struct Builder {
       e.grid = plan.take(grid.size() * 4);
       uploads.push_back(Upload{e.grid, std::move(grid)});
     }
-    // Workspace for max_images images.
-    const std::size_t M = e.max_images, P = enc::kMaxParts;
+    // Workspace for max_images images.  The partial-sum buffers hold, for every convolution and
+    // image count, its images' copies ([n][kMaxParts][C][H][W] layout: n * kMaxParts * C*H*W
+    // floats at most, and the split plan keeps n * parts * C*H*W within that).
+    const std::size_t M = e.max_images;
+    std::size_t stem_need = 0, conv_need = 0;
+    auto need = [&](const ConvW& c, int hin, int win) {
+      std::size_t m = 0;
+      for (std::size_t n = 1; n <= M; ++n) {
+        enc::ConvArgs a;
+        a.cin = c.cin;
+        a.cout = c.cout;
+        a.kh = a.kw = c.k;
+        a.stride = c.stride;
+        a.pad = c.pad;
+        a.hout = conv_out(hin, c.k, c.stride, c.pad);
+        a.wout = conv_out(win, c.k, c.stride, c.pad);
+        a.n = static_cast<int>(n);
+        enc::plan_conv(a);
+        const std::size_t act = static_cast<std::size_t>(c.cout) * a.hout * a.wout;
+        m = std::max(m, (n - 1) * enc::kMaxParts * act + a.ksplit * act);
+      }
+      return m;
+    };
+    stem_need = need(e.stem, L.vh, L.vw);
+    for (int s = 0; s < kStages; ++s)
+      for (int blk = 0; blk < kBlocks; ++blk) {
+        const BlockW& b = e.blocks[s][blk];
+        conv_need = std::max({conv_need, need(b.c1, b.hin, b.win), need(b.c2, b.hout, b.wout),
+                              b.proj ? need(b.ds, b.hin, b.win) : std::size_t{0}});
+      }
     e.images = plan.take(M * L.channels * img_h * img_w * 4);
-    e.stem_parts = plan.take(M * P * L.stem_c * L.stem_h * L.stem_w * 4);
+    e.stem_parts = plan.take(stem_need * 4);
     e.x0 = plan.take(M * act_max * 4);
     e.x1 = plan.take(M * act_max * 4);
     e.a1 = plan.take(M * act_max * 4);
-    e.h1 = plan.take(M * P * act_max * 4);
-    e.h2 = plan.take(M * P * act_max * 4);
-    e.hd = plan.take(M * P * act_max * 4);
+    e.h1 = plan.take(conv_need * 4);
+    e.h2 = plan.take(conv_need * 4);
+    e.hd = plan.take(conv_need * 4);
     e.features = plan.take(M * L.feature * 4);
+    e.kp = plan.take(M * 2 * L.keypoints * 4);
+    // GroupNorm statistics: the most (group, chunk) pairs of any pass (the stem's, whose groups
+    // hold the most values), 4 doubles each.
+    enc::NormArgs big;
+    big.c = 16;
+    big.groups = 1;
+    big.h = L.stem_h;
+    big.w = L.stem_w;
+    const std::size_t pairs = static_cast<std::size_t>(enc::norm_chunks(big)) * 32;
+    e.stats = plan.take(M * pairs * 4 * sizeof(double));
     return true;
   }
 };
@@ -382,6 +427,7 @@ hipError_t enqueue_encoder(FeEncoder& e, int n) {
   sn.beta = e.p(e.stem_n.beta);
   sn.dst = e.p(e.x0);
   sn.dst_stride = static_cast<std::int64_t>(L.stem_c) * L.pool_h * L.pool_w;
+  sn.stats = reinterpret_cast<double*>(e.arena + e.stats);
   FE_ENC_TRY(enc::norm(sn, e.stream));
   float* x = e.p(e.x0);
   float* nx = e.p(e.x1);
@@ -409,6 +455,7 @@ hipError_t enqueue_encoder(FeEncoder& e, int n) {
       m.beta = e.p(b.n1.beta);
       m.dst = e.p(e.a1);
       m.dst_stride = out_act;
+      m.stats = reinterpret_cast<double*>(e.arena + e.stats);
       FE_ENC_TRY(enc::norm(m, e.stream));
       FE_ENC_TRY(enqueue_conv(e, b.c2, e.p(e.a1), b.hout, b.wout, 0, 0, b.hout, b.wout, n,
                               e.p(e.h2), p2, s2, y2));
@@ -451,6 +498,7 @@ hipError_t enqueue_encoder(FeEncoder& e, int n) {
   h.grid = e.p(e.grid);
   h.out_w = e.p(e.out_w);
   h.out_b = e.p(e.out_b);
+  h.kp = e.p(e.kp);
   h.y = e.p(e.features);
   h.y_stride = L.feature;
   return enc::head(h, e.stream);

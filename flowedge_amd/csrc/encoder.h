@@ -9,14 +9,24 @@
 
 namespace fe::hip::enc {
 
-constexpr int kMaxParts = 8;  // partial sums of a split reduction
-constexpr std::size_t kMaxHeadLds = 160 * 1024;
+// Partial sums of a split reduction: up to 32 for outputs of at most kSmallOutput values (the
+// late, small-spatial layers, where adding them is cheap), up to 8 otherwise.
+constexpr int kMaxParts = 32;
+constexpr int kMaxPartsLarge = 8;
+constexpr std::int64_t kSmallOutput = 32768;
+constexpr int kMaxHeadPos = 1024;    // feature-map positions the keypoint head takes
+constexpr int kMaxHeadInputs = 1024; // keypoint coordinates (2 per keypoint) it takes
+
+// Reduction indices per step of the convolution; the weights are repacked step-major.
+constexpr int kReduceChunk = 16;
 
 // y (+ p * ypart for split p) = conv2d(x) of `n` images, no bias.  x is read through a view of
 // vh x vw pixels at (top, left) of each xh x xw input plane (the center crop of the stem);
 // padding `pad` zeros around the view.
 struct ConvArgs {
-  const float* w = nullptr;  // [cout][kh * kw][cin]
+  // [steps][cout][kReduceChunk]: w[s][o][j] is the weight of output o at reduction index
+  // k = s * kReduceChunk + j = tap * cin + input channel (zero for k >= kh * kw * cin).
+  const float* w = nullptr;
   const float* x = nullptr;
   std::int64_t xs = 0;       // floats between images
   std::int64_t xplane = 0;   // floats between channels (xh * xw)
@@ -44,9 +54,9 @@ enum NormMode : int {
   kNormEndGn = 3,     // dst = relu(GN(src) + GN_r(res))          (1x1 projection residual)
 };
 
-// One workgroup per (image, group) of `groups` GroupNorm groups over c channels of h x w.  src
-// (and res in kNormEndGn) are sums of `parts` partials, which the pass adds (writing the sum over
-// the first partial) before the statistics.
+// GroupNorm with `groups` groups over c channels of h x w of n images.  src (and res in
+// kNormEndGn) are sums of `parts` partials, which the pass adds (writing the sum over the first
+// partial) before the statistics.
 struct NormArgs {
   int mode = kNormMid;
   int n = 0, c = 0, h = 0, w = 0, groups = 0;
@@ -64,12 +74,18 @@ struct NormArgs {
   const float* rbeta = nullptr;
   float* dst = nullptr;
   std::int64_t dst_stride = 0;
+  double* stats = nullptr;  // workspace of norm_chunks(a) * 4 doubles per (image, group)
 };
+// Statistics workgroups per (image, group) of the pass.
+int norm_chunks(const NormArgs& a);
+// One launch for groups of at most 8192 values outside the stem mode (a workgroup per group);
+// else two: fp64 statistics per chunk of each group (adding the partials), then one lane per
+// output value.
 hipError_t norm(const NormArgs& a, hipStream_t stream);
 
 // Per image: keypoint logits = nets_w [k][c] x (feature maps [c][hw]) + nets_b, softmax over the
-// hw positions, expected (x, y) on grid [hw][2], then y = relu(out_w [fout][2k] kp + out_b),
-// written at y + image * y_stride + y_offset.
+// hw positions, expected (x, y) on grid [hw][2] into kp [n][2k] (workspace), then
+// y = relu(out_w [fout][2k] kp + out_b), written at y + image * y_stride + y_offset.
 struct HeadArgs {
   const float* x = nullptr;
   std::int64_t x_stride = 0;
@@ -79,10 +95,10 @@ struct HeadArgs {
   const float* grid = nullptr;
   const float* out_w = nullptr;
   const float* out_b = nullptr;
+  float* kp = nullptr;
   float* y = nullptr;
   std::int64_t y_stride = 0, y_offset = 0;
 };
-std::size_t head_lds_bytes(int c, int hw, int k);
 hipError_t head(const HeadArgs& a, hipStream_t stream);
 
 }  // namespace fe::hip::enc
