@@ -20,7 +20,9 @@
 // group_norm :270-350, film :352-377.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "conv_mfma.h"
 #include "device_common.h"
@@ -253,24 +255,55 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
           P[(wr * S::WM + 16 * i + 4 * kq + e) * NT + wc * S::WN + 16 * j + l16] = acc[i][j][e];
     return;
   }
+  // Output layout: when the tile fits the staging LDS it goes through it as [sample, position]
+  // [channel], so that each sample's MT x LOUT block (contiguous in y) is written by
+  // consecutive lanes.
+  constexpr int TROW = MT + 1;
+  if constexpr (NT * TROW <= 2 * (S::WFLOATS + S::XFLOATS)) {
+    float* T = reinterpret_cast<float*>(lds4);
+    __syncthreads();  // the last K step's LDS reads are done
 #pragma unroll
-  for (int i = 0; i < S::TI; ++i)
+    for (int j = 0; j < S::TJ; ++j) {
+      const int col = wc * S::WN + 16 * j + l16;
+      int bl, t;
+      col_pos(col, NT, S::LOUT, PAR, bl, t);
+      float* tr = T + (bl * S::LOUT + t) * TROW + wr * S::WM + 4 * kq;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
-      if (oc >= a.oc) continue;
-      const float bias = ks == 0 ? a.bias[oc] : 0.0f;
+      for (int i = 0; i < S::TI; ++i)
 #pragma unroll
-      for (int j = 0; j < S::TJ; ++j) {
-        const int col = wc * S::WN + 16 * j + l16;
-        int bl, t;
-        col_pos(col, NT, S::LOUT, PAR, bl, t);
-        const int b = b0 + bl;
-        if (b < a.batch)
-          a.y[ks * a.ypart + b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
-              acc[i][j][e] + bias;
-      }
+        for (int e = 0; e < 4; ++e) tr[16 * i + e] = acc[i][j][e];
     }
+    __syncthreads();
+    float* yk = a.y + ks * a.ypart;
+    for (int idx = tid; idx < NT * MT; idx += kMmThreads) {
+      const int bl = idx / (MT * S::LOUT);
+      const int rem = idx - bl * (MT * S::LOUT);
+      const int row = rem / S::LOUT, t = rem - row * S::LOUT;
+      const int b = b0 + bl, oc = m0 + row;
+      if (b < a.batch && oc < a.oc)
+        yk[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
+            T[(bl * S::LOUT + t) * TROW + row] + (ks == 0 ? a.bias[oc] : 0.0f);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
+        if (oc >= a.oc) continue;
+        const float bias = ks == 0 ? a.bias[oc] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < S::TJ; ++j) {
+          const int col = wc * S::WN + 16 * j + l16;
+          int bl, t;
+          col_pos(col, NT, S::LOUT, PAR, bl, t);
+          const int b = b0 + bl;
+          if (b < a.batch)
+            a.y[ks * a.ypart + b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
+                acc[i][j][e] + bias;
+        }
+      }
+  }
 }
 
 // Sums the ksplit partial tiles of a split-K convolution in a fixed order and adds the bias.
@@ -470,14 +503,33 @@ struct MmPlan {
   std::uint64_t wb = 0, sb = 0, pb = 0;
 };
 
+// Tuning overrides, read once: FLOWEDGE_MM_TILE=64|128 forces the column tile (64 x 64 or
+// 64 x 128 blocks; narrow inputs always take 64 x 64), FLOWEDGE_MM_WGS the workgroup count the
+// K split aims at (default 512, two per CU).
+struct MmTuning {
+  int tile = 0;
+  int target = 512;
+};
+const MmTuning& mm_tuning() {
+  static const MmTuning t = [] {
+    MmTuning m;
+    if (const char* v = std::getenv("FLOWEDGE_MM_TILE")) m.tile = std::atoi(v);
+    if (const char* v = std::getenv("FLOWEDGE_MM_WGS")) m.target = std::max(1, std::atoi(v));
+    return m;
+  }();
+  return t;
+}
+
 MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
                std::int64_t plain_stride, int batch, std::size_t workspace_floats, bool bf16_mma,
                bool f32_split, int max_parts) {
+  const MmTuning& tune = mm_tuning();
   MmPlan p;
   p.narrow = op.ic % kKC != 0;
   p.mtiles = (op.oc + 63) / 64;
   p.ntiles = (batch + 128 / op.lout - 1) / (128 / op.lout);
-  if (p.narrow || p.mtiles * p.ntiles < 256) {
+  const bool small = tune.tile == 64 || (tune.tile != 128 && p.mtiles * p.ntiles < 256);
+  if (p.narrow || small) {
     p.tile = kTile64x64;
     p.ntiles = (batch + 64 / op.lout - 1) / (64 / op.lout);
   }
@@ -492,8 +544,8 @@ MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float
   const int nsteps = p.use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
   // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
   // workgroups per CU, so that two K steps of weights stream per CU at a time.
-  if (tiles < 256) {
-    int ks = (512 + tiles - 1) / tiles;
+  if (tiles < tune.target / 2) {
+    int ks = (tune.target + tiles - 1) / tiles;
     if (ks > nsteps) ks = nsteps;
     if (max_parts >= 2) {
       if (ks > max_parts) ks = max_parts;

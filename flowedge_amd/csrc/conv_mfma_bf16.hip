@@ -302,6 +302,8 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   };
 
   // K loop: the next step's loads are in flight while the matrix cores work on the current one.
+  // (Three steps in flight, in rotating register sets, measured slower at B=64: 21.9 against
+  // 20.8 us for the 2048<-2048 L2 layer.)
   Regs rn;
   load_step(s0, rn);
   store_step(0, rn);
@@ -326,24 +328,34 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
           P[(wr * S::WM + 16 * i + 4 * kq + e) * NT + wc * S::WN + 16 * j + l16] = acc[i][j][e];
     return;
   }
+  // Output layout: the tile goes through LDS as [sample, position][channel], so that each
+  // sample's MT x LOUT block (contiguous in y) is written by consecutive lanes.
+  constexpr int TROW = MT + 1;
+  static_assert(static_cast<std::size_t>(NT) * TROW * 4 <= S::LDS_BYTES, "epilogue tile in LDS");
+  float* T = reinterpret_cast<float*>(lds_b);
+  __syncthreads();  // the last K step's LDS reads are done
 #pragma unroll
-  for (int i = 0; i < S::TI; ++i)
+  for (int j = 0; j < S::TJ; ++j) {
+    const int col = wc * S::WN + 16 * j + l16;
+    int bl2, t;
+    col_pos(col, NT, S::LOUT, PAR, bl2, t);
+    float* tr = T + (bl2 * S::LOUT + t) * TROW + wr * S::WM + 4 * kq;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
-      if (oc >= a.oc) continue;
-      const float bias = ks == 0 ? a.bias[oc] : 0.0f;
+    for (int i = 0; i < S::TI; ++i)
 #pragma unroll
-      for (int j = 0; j < S::TJ; ++j) {
-        const int col = wc * S::WN + 16 * j + l16;
-        int bl2, t;
-        col_pos(col, NT, S::LOUT, PAR, bl2, t);
-        const int b = b0 + bl2;
-        if (b < a.batch)
-          a.y[ks * a.ypart + b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
-              acc[i][j][e] + bias;
-      }
-    }
+      for (int e = 0; e < 4; ++e) tr[16 * i + e] = acc[i][j][e];
+  }
+  __syncthreads();
+  float* yk = a.y + ks * a.ypart;
+  for (int idx = tid; idx < NT * MT; idx += kBThreads) {
+    const int bl2 = idx / (MT * S::LOUT);
+    const int rem = idx - bl2 * (MT * S::LOUT);
+    const int row = rem / S::LOUT, t = rem - row * S::LOUT;
+    const int b = b0 + bl2, oc = m0 + row;
+    if (b < a.batch && oc < a.oc)
+      yk[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
+          T[(bl2 * S::LOUT + t) * TROW + row] + (ks == 0 ? a.bias[oc] : 0.0f);
+  }
 }
 
 template <int MODE, int K, int LIN, int MT, int NT, bool WF32>
