@@ -50,15 +50,20 @@ struct BShape {
   static constexpr int WUNITS = MT * K * (kKCB / (WF32 ? 4 : 8));  // weight units per step
   static constexpr int UW = (WUNITS + kBThreads - 1) / kBThreads;
   static constexpr int WARR = WF32 ? 2 : 1;  // weight arrays in LDS (hi, lo)
-  static constexpr int XP = LIN >= 4 ? 4 : LIN;   // positions per input load
-  static constexpr int NTQ = LIN / XP;              // position groups per sample
-  static constexpr int XUNITS8 = SB * NTQ * 4;      // input units (8 channels x XP positions)
+  // Input units: CPU channels x PPU positions of one sample, read as contiguous 16-byte vectors
+  // of its [channel][position] block (LIN = 1: 4 channels; 2: 2 channels x 2 positions; >= 4:
+  // 2 channels x 4 positions, two vectors).
+  static constexpr int CPU = LIN == 1 ? 4 : 2;
+  static constexpr int PPU = LIN >= 4 ? 4 : LIN;
+  static constexpr int XVEC = LIN >= 4 ? 2 : 1;     // 16-byte loads per unit
+  static constexpr int UPS = (kKCB / CPU) * (LIN / PPU);  // units per sample and step
+  static constexpr int XUNITS = SB * UPS;
   static constexpr int WM = MT / kWaveRows, WN = NT / kWaveCols;
   static constexpr int TI = WM / 16, TJ = WN / 16;
   static constexpr std::size_t LDS_BYTES = (2 * WARR * WVALS + 4 * XVALS) * 2;
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wavefront tiles of 16 x 16 MFMA blocks");
   static_assert(NT % LOUT == 0, "column tile");
-  static constexpr int UXN = (XUNITS8 + kBThreads - 1) / kBThreads;  // input units per lane
+  static constexpr int UXN = (XUNITS + kBThreads - 1) / kBThreads;  // input units per lane
   static_assert(WROW % 8 == 0 && XROW % 8 == 0, "16-byte LDS rows");
 };
 
@@ -132,26 +137,27 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
                                 : kOutOfRange;
     wlds[r] = act ? m * S::WROW + k * kKCB + QW * q : -1;
   }
-  // Input units: 8 channels x P positions of one sample (P = min(LIN, 4)), loaded as 8 vectors of
-  // P floats (channels are LIN floats apart) and stored as P rows of 8 BF16 values per term.
-  constexpr int P = S::XP;
+  // Input units (see BShape): consecutive lanes read consecutive 16-byte pieces of a sample's
+  // 32-channel block, and each unit is stored as PPU rows (positions) of CPU BF16 channels per
+  // term.
   int xlds[S::UXN];
   unsigned xvs[S::UXN], xvp[S::UXN];
 #pragma unroll
   for (int n = 0; n < S::UXN; ++n) {
     const int uu = tid + n * kBThreads;
-    const bool act = uu < S::XUNITS8;
+    const bool act = uu < S::XUNITS;
     const int u = act ? uu : 0;
-    const int bl = u / (S::NTQ * 4), v = u - bl * (S::NTQ * 4);
-    const int tq = v / 4, cg = v - tq * 4;
+    const int bl = u / S::UPS, v = u - bl * S::UPS;
+    const int tq = v % (LIN / S::PPU), cg = v / (LIN / S::PPU);
+    const int c = cg * S::CPU, t0 = tq * S::PPU;
     const int b = b0 + bl;
-    xlds[n] = act ? (bl * LIN + tq * P) * S::XROW + 8 * cg : -1;
+    xlds[n] = act ? (bl * LIN + t0) * S::XROW + c : -1;
     xvs[n] = kOutOfRange;
     xvp[n] = kOutOfRange;
     if (act && b < a.batch) {
-      xvs[n] = static_cast<unsigned>((b * a.src_stride + 8 * cg * LIN + tq * P) * 4);
+      xvs[n] = static_cast<unsigned>((b * a.src_stride + c * LIN + t0) * 4);
       if (a.plain != nullptr)
-        xvp[n] = static_cast<unsigned>((b * a.plain_stride + 8 * cg * LIN + tq * P) * 4);
+        xvp[n] = static_cast<unsigned>((b * a.plain_stride + c * LIN + t0) * 4);
     }
   }
   const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(a.src, a.srcbytes);
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   // One K step's staged data in registers.
   struct Regs {
     uint4 w[S::UW];
-    float x[S::UXN][8][P];
+    float4 x[S::UXN][S::XVEC];
   };
   auto load_step = [&](int step, Regs& R) {
     const int ic0 = step * kKCB;
@@ -175,25 +181,10 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     for (int n = 0; n < S::UXN; ++n) {
       const unsigned xv = from_src ? xvs[n] : xvp[n];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const unsigned so = xs0 + static_cast<unsigned>(j * LIN * 4);
-        if constexpr (P == 4) {
-          const float4 v =
-              __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xv, so, 0));
-          R.x[n][j][0] = v.x;
-          R.x[n][j][1] = v.y;
-          R.x[n][j][2] = v.z;
-          R.x[n][j][3] = v.w;
-        } else if constexpr (P == 2) {
-          const float2 v =
-              __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(xrs, xv, so, 0));
-          R.x[n][j][0] = v.x;
-          R.x[n][j][1] = v.y;
-        } else {
-          R.x[n][j][0] =
-              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xv, so, 0));
-        }
-      }
+      for (int j = 0; j < S::XVEC; ++j)
+        R.x[n][j] = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(
+                        xrs, xv, xs0 + static_cast<unsigned>(j * LIN * 4), 0));
     }
   };
   auto store_step = [&](int buf, const Regs& R) {
@@ -218,20 +209,33 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     }
 #pragma unroll
     for (int n = 0; n < S::UXN; ++n) {
-      if (xlds[n] < 0) continue;
+      if (S::XUNITS % kBThreads != 0 && xlds[n] < 0) continue;
       unsigned short* H = Xh + buf * S::XVALS + xlds[n];
       unsigned short* L = Xl + buf * S::XVALS + xlds[n];
+      // Value of channel c (0 .. CPU-1) at position p (0 .. PPU-1) of the unit.
+      auto val = [&](int c, int p) {
+        const float4& v = R.x[n][LIN >= 4 ? c : 0];
+        const int e = LIN >= 4 ? p : c * LIN + p;
+        return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+      };
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        bf16x8 hv, lv;
+      for (int p = 0; p < S::PPU; ++p) {
+        unsigned short hb[S::CPU], lb[S::CPU];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const __bf16 h = static_cast<__bf16>(R.x[n][j][p]);
-          hv[j] = h;
-          lv[j] = static_cast<__bf16>(R.x[n][j][p] - static_cast<float>(h));
+        for (int c = 0; c < S::CPU; ++c) split_bf16(val(c, p), hb[c], lb[c]);
+        if constexpr (S::CPU == 4) {
+          *reinterpret_cast<uint2*>(H + p * S::XROW) =
+              uint2{hb[0] | (static_cast<unsigned>(hb[1]) << 16),
+                    hb[2] | (static_cast<unsigned>(hb[3]) << 16)};
+          *reinterpret_cast<uint2*>(L + p * S::XROW) =
+              uint2{lb[0] | (static_cast<unsigned>(lb[1]) << 16),
+                    lb[2] | (static_cast<unsigned>(lb[3]) << 16)};
+        } else {
+          *reinterpret_cast<unsigned*>(H + p * S::XROW) =
+              hb[0] | (static_cast<unsigned>(hb[1]) << 16);
+          *reinterpret_cast<unsigned*>(L + p * S::XROW) =
+              lb[0] | (static_cast<unsigned>(lb[1]) << 16);
         }
-        *reinterpret_cast<uint4*>(H + p * S::XROW) = __builtin_bit_cast(uint4, hv);
-        *reinterpret_cast<uint4*>(L + p * S::XROW) = __builtin_bit_cast(uint4, lv);
       }
     }
   };
