@@ -343,6 +343,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the bimanual and flow configs")
+    ap.add_argument("--no-split", action="store_true",
+                    help="skip the large batch on the BF16 matrix cores with split F32 operands")
     ap.add_argument("--roofline-iters", type=int, default=200,
                     help="rounds over the dominant convolution's layers")
     ap.add_argument("--roofline-only", action="store_true",
@@ -501,6 +503,50 @@ def main():
                   f"  {r.get('tflops', 0):6.1f} TFLOP/s  {r['us_per_nfe']:9.1f} us/NFE",
                   file=sys.stderr, flush=True)
         large["conv_breakdown"] = [{k: v for k, v in r.items() if k != "indices"} for r in bd_large]
+
+        # The same batch with F32 weights and inputs each split into two BF16 terms on the BF16
+        # matrix cores (opt-in FLOWEDGE_MFMA_F32_SPLIT=1 at load: Wh Xh + Wh Xl + Wl Xh per
+        # product, the Wl Xl term of ~2^-16 relative dropped, fp32 accumulation).  Reported beside
+        # the exact-F32 line above, with its own error against the oracle on the same rows.
+        if not args.no_split:
+            os.environ["FLOWEDGE_MFMA_F32_SPLIT"] = "1"
+            try:
+                eng_s = flowedge_amd.Engine(path)
+            finally:
+                del os.environ["FLOWEDGE_MFMA_F32_SPLIT"]
+            eng_s.prepare(0, B, steps_ddim, 0)
+
+            def tick_s():
+                eng_s.sample_device(0, d_cb.data_ptr(), d_nb.data_ptr(), B, steps_ddim, 0, 0,
+                                    d_ob.data_ptr())
+
+            tick_s()
+            torch.cuda.synchronize()
+            sl, sd = [], []
+            for _ in range(args.large_steps):
+                t0 = time.perf_counter()
+                tick_s()
+                sl.append((time.perf_counter() - t0) * 1e3)
+                sd.append(eng_s.last_device_ms)
+            sp50 = percentile(sl, 50)
+            out_s = d_ob.cpu().numpy()
+            err_s = oracle_check(path, cb, nb, out_s, steps_ddim, sub) if not args.no_cpu else None
+            useful = flops_tick / (percentile(sd, 50) / 1e3) / 1e12
+            large["f32_split_bf16_mfma"] = {
+                "p50_ms": sp50, "device_p50_ms": percentile(sd, 50),
+                "actions_per_sec": B * spec.horizon / (sp50 / 1e3),
+                "useful_tflops": useful,
+                "bf16_mfma_frac": 3 * useful / BF16_MFMA_PEAK_TFLOPS,
+                "finite": bool(np.all(np.isfinite(out_s))),
+                "max_abs_err_vs_oracle": err_s,
+                "oracle_samples": sub,
+                "arithmetic": "F32 weights and inputs split into BF16 hi + lo terms, three BF16 "
+                              "MFMA products (hi*hi + hi*lo + lo*hi), fp32 accumulation; opt-in "
+                              "FLOWEDGE_MFMA_F32_SPLIT=1",
+            }
+            print(f"[bench] B={B} DDIM-10 tick p50 {sp50:.2f} ms on BF16 matrix cores with split "
+                  f"F32 operands (max err {err_s})", file=sys.stderr, flush=True)
+            eng_s.close()
 
     breakdown = conv_breakdown(eng, batch=1)
     for r in breakdown:
