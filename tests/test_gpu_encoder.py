@@ -55,6 +55,24 @@ def test_encoder_matches_oracle(enc_path, n):
         assert err <= TOL
 
 
+@pytest.mark.parametrize("image_hw,crop_hw", [((120, 160), None), ((97, 85), (84, 84))])
+def test_encoder_other_geometries(tmp_path, image_hw, crop_hw):
+    # A wide camera without a crop (odd feature-map sizes through every stride-2 stage: 60x80,
+    # 30x40, 15x20, 8x10, 4x5) and odd crop margins (torchvision rounds 6.5 down to 6, 0.5 to 0).
+    spec = ck.EncoderSpec(image_hw=image_hw, crop_hw=crop_hw)
+    path = str(tmp_path / "enc.safetensors")
+    ck.write_safetensors(path, ck.synthetic_encoder_tensors(spec))
+    images = ck.encoder_images(spec, 2, seed=13)
+    t = oracle_tensors(path)
+    with RgbEncoder(path, image_hw=image_hw, crop_hw=crop_hw, max_images=2) as e:
+        got = e.encode(images)
+    for i in range(2):
+        want = er.encode(t, images[i], crop_hw)
+        err = float(np.abs(got[i] - want).max())
+        say(f"{image_hw} crop {crop_hw} image {i}: max |err| {err:.3e}")
+        assert err <= TOL
+
+
 def test_encoder_device_output_lands_in_condition_layout(enc_path):
     spec = ck.EncoderSpec()
     images = ck.encoder_images(spec, 2, seed=11)
