@@ -16,7 +16,7 @@ constexpr int kMmThreads = 256;
 
 // Column tiles: 64 output channels x 128 columns, or 64 x 64 when the larger column tile would
 // leave CUs without a workgroup.
-enum MmTile : int { kTile64x128 = 0, kTile64x64 = 1 };
+enum MmTile : int { kTile64x128 = 0, kTile64x64 = 1, kTile64x32 = 2 };
 
 __host__ __device__ constexpr int lout_for(int mode, int lin) {
   return mode == kConvSame ? lin : (mode == kConvDown ? lin / 2 : 2 * lin);

@@ -503,9 +503,9 @@ struct MmPlan {
   std::uint64_t wb = 0, sb = 0, pb = 0;
 };
 
-// Tuning overrides, read once: FLOWEDGE_MM_TILE=64|128 forces the column tile (64 x 64 or
-// 64 x 128 blocks; narrow inputs always take 64 x 64), FLOWEDGE_MM_WGS the workgroup count the
-// K split aims at (default 512, two per CU).
+// Tuning overrides, read once: FLOWEDGE_MM_TILE=32|64|128 forces the column tile (64 x 32 for
+// BF16 weights only, 64 x 64 or 64 x 128 blocks; narrow inputs always take 64 x 64),
+// FLOWEDGE_MM_WGS the workgroup count the K split aims at (default 512, two per CU).
 struct MmTuning {
   int tile = 0;
   int target = 512;
@@ -534,13 +534,22 @@ MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float
     p.ntiles = (batch + 64 / op.lout - 1) / (64 / op.lout);
   }
   p.nt_cols = p.tile == kTile64x128 ? 128 : 64;
-  const int tiles = p.mtiles * p.ntiles;
   // The BF16 kernels address weights and inputs through 32-bit buffer offsets.
   p.wb = static_cast<std::uint64_t>(op.oc) * op.k * op.ic * (op.bf16 ? 2 : 4);
   p.sb = static_cast<std::uint64_t>(batch) * src_stride * 4;
   p.pb = plain != nullptr ? static_cast<std::uint64_t>(batch) * plain_stride * 4 : 0;
   const bool ranges_fit = p.wb < (1ull << 31) && p.sb < (1ull << 31) && p.pb < (1ull << 31);
   p.use_bf16 = (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
+  // BF16 weights with fewer than 64 tiles of 64 x 64: 64 x 32 blocks, so that the split K loop
+  // runs on twice the workgroups (two per CU, whose K steps overlap), and a batch that fills
+  // under 64 columns leaves none of them empty.
+  if (p.use_bf16 && op.bf16 && p.tile == kTile64x64 && !p.narrow &&
+      (tune.tile == 32 || (tune.tile == 0 && p.mtiles * p.ntiles < 64))) {
+    p.tile = kTile64x32;
+    p.nt_cols = 32;
+    p.ntiles = (batch + 32 / op.lout - 1) / (32 / op.lout);
+  }
+  const int tiles = p.mtiles * p.ntiles;
   const int nsteps = p.use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
   // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
   // workgroups per CU, so that two K steps of weights stream per CU at a time.

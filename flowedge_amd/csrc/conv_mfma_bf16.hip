@@ -384,6 +384,7 @@ hipError_t by_tile(int tile, bool wf32, const MmArgs& a, hipStream_t s) {
   if (wf32)
     return tile == kTile64x128 ? launch<MODE, K, LIN, 64, 128, true>(a, s)
                                : launch<MODE, K, LIN, 64, 64, true>(a, s);
+  if (tile == kTile64x32) return launch<MODE, K, LIN, 64, 32, false>(a, s);
   return tile == kTile64x128 ? launch<MODE, K, LIN, 64, 128, false>(a, s)
                              : launch<MODE, K, LIN, 64, 64, false>(a, s);
 }
