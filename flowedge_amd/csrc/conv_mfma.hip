@@ -430,6 +430,7 @@ hipError_t by_tile(int tile, bool narrow, const MmArgs& a, hipStream_t s) {
     if constexpr (MODE == kConvSame) return launch_mm<MODE, K, LIN, BF16, 64, 64, true>(a, s);
     return hipErrorInvalidValue;
   }
+  if (tile == kTile64x32) return launch_mm<MODE, K, LIN, BF16, 64, 32, false>(a, s);
   return tile == kTile64x128 ? launch_mm<MODE, K, LIN, BF16, 64, 128, false>(a, s)
                              : launch_mm<MODE, K, LIN, BF16, 64, 64, false>(a, s);
 }
@@ -503,8 +504,8 @@ struct MmPlan {
   std::uint64_t wb = 0, sb = 0, pb = 0;
 };
 
-// Tuning overrides, read once: FLOWEDGE_MM_TILE=32|64|128 forces the column tile (64 x 32 for
-// BF16 weights only, 64 x 64 or 64 x 128 blocks; narrow inputs always take 64 x 64),
+// Tuning overrides, read once: FLOWEDGE_MM_TILE=32|64|128 forces the column tile (64 x 32,
+// 64 x 64 or 64 x 128 blocks; narrow inputs always take 64 x 64),
 // FLOWEDGE_MM_WGS the workgroup count the K split aims at (default 512, two per CU).
 struct MmTuning {
   int tile = 0;
@@ -540,10 +541,11 @@ MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float
   p.pb = plain != nullptr ? static_cast<std::uint64_t>(batch) * plain_stride * 4 : 0;
   const bool ranges_fit = p.wb < (1ull << 31) && p.sb < (1ull << 31) && p.pb < (1ull << 31);
   p.use_bf16 = (op.bf16 ? bf16_mma : f32_split) && ranges_fit && mm_bf16_ok(op, split);
-  // BF16 weights with fewer than 64 tiles of 64 x 64: 64 x 32 blocks, so that the split K loop
-  // runs on twice the workgroups (two per CU, whose K steps overlap), and a batch that fills
-  // under 64 columns leaves none of them empty.
-  if (p.use_bf16 && op.bf16 && p.tile == kTile64x64 && !p.narrow &&
+  // Fewer than 64 tiles of 64 x 64: 64 x 32 blocks, so that the split K loop runs on twice the
+  // workgroups (two per CU, whose K steps overlap), and a batch that fills under 64 columns
+  // leaves none of them empty.  (Not for F32 weights on the BF16 matrix cores, which have no
+  // 64 x 32 instance.)
+  if (!(p.use_bf16 && !op.bf16) && p.tile == kTile64x64 && !p.narrow &&
       (tune.tile == 32 || (tune.tile == 0 && p.mtiles * p.ntiles < 64))) {
     p.tile = kTile64x32;
     p.nt_cols = 32;
