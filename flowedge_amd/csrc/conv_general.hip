@@ -230,11 +230,12 @@ __device__ __forceinline__ float part_sum(const float* p, int parts, std::int64_
 }
 
 constexpr int kNgRegs = 8;  // region values kept in registers between the two passes
+constexpr int kNaThreads = 512;  // lanes of the per-(sample, group) GroupNorm pass
 
-__global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput in, int lin,
+__global__ __launch_bounds__(kNaThreads) void norm_act_general_kernel(ConvInput in, int lin,
                                                                       float* dst,
                                                                       std::int64_t dst_stride) {
-  __shared__ double rs[kNgThreads / kWave], rq[kNgThreads / kWave];
+  __shared__ double rs[kNaThreads / kWave], rq[kNaThreads / kWave];
   const int b = blockIdx.x / in.groups, g = blockIdx.x % in.groups;
   const int cpg = in.split / in.groups;
   const int n = cpg * lin;
@@ -247,13 +248,13 @@ __global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput 
   double s = 0.0, q = 0.0;
 #pragma unroll
   for (int r = 0; r < kNgRegs; ++r) {
-    const int i = tid + r * kNgThreads;
+    const int i = tid + r * kNaThreads;
     v[r] = i < n ? part_sum(src + i, in.parts, in.part_stride) : 0.0f;
     const double d = static_cast<double>(v[r]);
     s += d;
     q += d * d;
   }
-  for (int i = tid + kNgRegs * kNgThreads; i < n; i += kNgThreads) {
+  for (int i = tid + kNgRegs * kNaThreads; i < n; i += kNaThreads) {
     const double d = static_cast<double>(part_sum(src + i, in.parts, in.part_stride));
     s += d;
     q += d * d;
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput 
   __syncthreads();
   s = 0.0;
   q = 0.0;
-  for (int w = 0; w < kNgThreads / kWave; ++w) {
+  for (int w = 0; w < kNaThreads / kWave; ++w) {
     s += rs[w];
     q += rq[w];
   }
@@ -290,10 +291,10 @@ __global__ __launch_bounds__(kNgThreads) void norm_act_general_kernel(ConvInput 
   };
 #pragma unroll
   for (int r = 0; r < kNgRegs; ++r) {
-    const int i = tid + r * kNgThreads;
+    const int i = tid + r * kNaThreads;
     if (i < n) put(i, v[r]);
   }
-  for (int i = tid + kNgRegs * kNgThreads; i < n; i += kNgThreads)
+  for (int i = tid + kNgRegs * kNaThreads; i < n; i += kNaThreads)
     put(i, part_sum(src + i, in.parts, in.part_stride));
 }
 
@@ -373,7 +374,7 @@ hipError_t norm_act_general(const ConvInput& in, int lin, float* dst, std::int64
   const std::int64_t blocks = static_cast<std::int64_t>(batch) * in.groups;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL(norm_act_general_kernel, dim3(static_cast<unsigned>(blocks)),
-                     dim3(kNgThreads), 0, stream, in, lin, dst, dst_stride);
+                     dim3(kNaThreads), 0, stream, in, lin, dst, dst_stride);
   return hipGetLastError();
 }
 
