@@ -314,9 +314,9 @@ struct Builder {
       e.grid = plan.take(grid.size() * 4);
       uploads.push_back(Upload{e.grid, std::move(grid)});
     }
-    // Workspace for max_images images.  The partial-sum buffers hold, for every convolution and
-    // image count, its images' copies ([n][kMaxParts][C][H][W] layout: n * kMaxParts * C*H*W
-    // floats at most, and the split plan keeps n * parts * C*H*W within that).
+    // Workspace for max_images images.  A convolution's partial sums are laid out
+    // [part][image][C][H][W]; the buffers hold the largest parts * n * C*H*W of any convolution
+    // at any image count n (large image counts need no split).
     const std::size_t M = e.max_images;
     std::size_t stem_need = 0, conv_need = 0;
     auto need = [&](const ConvW& c, int hin, int win) {
@@ -333,7 +333,7 @@ struct Builder {
         a.n = static_cast<int>(n);
         enc::plan_conv(a);
         const std::size_t act = static_cast<std::size_t>(c.cout) * a.hout * a.wout;
-        m = std::max(m, (n - 1) * enc::kMaxParts * act + a.ksplit * act);
+        m = std::max(m, static_cast<std::size_t>(a.ksplit) * n * act);
       }
       return m;
     };
@@ -396,8 +396,8 @@ hipError_t enqueue_conv(FeEncoder& e, const ConvW& c, const float* x, int xh, in
   a.wout = conv_out(vw, c.k, c.stride, c.pad);
   a.n = n;
   enc::plan_conv(a);
-  part = static_cast<std::int64_t>(c.cout) * a.hout * a.wout;
-  ys = part * enc::kMaxParts;
+  ys = static_cast<std::int64_t>(c.cout) * a.hout * a.wout;
+  part = ys * n;
   a.y = y;
   a.ys = ys;
   a.ypart = part;

@@ -10,7 +10,7 @@
 // end), so one step of a workgroup reads 4 KB of contiguous weights, and the 3-channel stem
 // takes 10 steps rather than 49.  When the output tiles leave CUs idle, the
 // reduction is split over workgroups and each writes its partial sum into its own copy of the
-// output ([n][parts][C][H][W]); the GroupNorm pass that consumes the convolution adds the
+// output ([parts][n][C][H][W]); the GroupNorm pass that consumes the convolution adds the
 // partials in order.  The convolutions carry no bias.
 //
 // The GroupNorm pass finishes a convolution.  Groups of at most kFusedMax values (every block

@@ -73,6 +73,22 @@ def test_encoder_other_geometries(tmp_path, image_hw, crop_hw):
         assert err <= TOL
 
 
+def test_encoder_largest_image_count(enc_path):
+    # 64 images (the most one call takes): no split reduction at this count, the workspace
+    # planned for it; the first, a middle and the last image against the oracle.
+    spec = ck.EncoderSpec()
+    images = ck.encoder_images(spec, 64, seed=17)
+    t = oracle_tensors(enc_path)
+    with RgbEncoder(enc_path, max_images=64) as e:
+        got = e.encode(images)
+        say(f"encoder n=64: {e.last_device_ms:.3f} ms, arena {e.device_bytes / 2**20:.1f} MiB")
+    for i in (0, 31, 63):
+        want = er.encode(t, images[i], spec.crop_hw)
+        err = float(np.abs(got[i] - want).max())
+        say(f"image {i}: max |err| {err:.3e}")
+        assert err <= TOL
+
+
 def test_encoder_device_output_lands_in_condition_layout(enc_path):
     spec = ck.EncoderSpec()
     images = ck.encoder_images(spec, 2, seed=11)
