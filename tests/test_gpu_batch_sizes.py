@@ -43,7 +43,7 @@ def check_all(got, want, label):
     assert err[worst] <= TOL
 
 
-def test_pusht_b256_ddim10(ckpt_dir):
+def test_pusht_b256_ddim10(ckpt_dir, monkeypatch):
     spec = ck.SPECS["pusht"]
     path = ck.cached_checkpoint("pusht", ckpt_dir)
     B = 256
@@ -51,11 +51,17 @@ def test_pusht_b256_ddim10(ckpt_dir):
     say(f"pusht DDIM-10 B={B}: GPU")
     with flowedge_amd.Engine(path) as e:
         got = e.sample_diffusion_batch(cond, noise, steps=10)
+    # The opt-in split-F32 path (F32 operands as BF16 hi + lo terms on the BF16 matrix cores)
+    # at the same batch, against the same oracle samples.
+    monkeypatch.setenv("FLOWEDGE_MFMA_F32_SPLIT", "1")
+    with flowedge_amd.Engine(path) as e:
+        got_split = e.sample_diffusion_batch(cond, noise, steps=10)
     t0 = time.time()
     want = oracle.Oracle(path).sample_batch(cond, noise, 10, workers=WORKERS)
     say(f"pusht DDIM-10 B={B}: oracle {time.time() - t0:.1f} s")
     check_all(got, want, f"pusht DDIM-10 B={B}")
     assert np.all(got >= -1.0) and np.all(got <= 1.0)
+    check_all(got_split, want, f"pusht DDIM-10 B={B} split-F32")
 
 
 def test_bimanual_bf16_b64_ddim10(ckpt_dir):
