@@ -129,6 +129,31 @@ def conv_breakdown(eng, batch: int = 1, iters: int = 50):
     return rows
 
 
+def encoder_timing(n: int, iters: int = 30) -> dict:
+    """The observation encoder (resnet18-GroupNorm + keypoints, fe_encoder_encode) on n synthetic
+    96 x 96 camera images center-cropped to 84 x 84: device time of its graph (hipEvents)."""
+    import numpy as np
+
+    from flowedge_amd import checkpoint as ck
+    from flowedge_amd.encoder import RgbEncoder
+
+    spec = ck.EncoderSpec()
+    images = ck.encoder_images(spec, n)
+    with RgbEncoder(ck.cached_encoder(), max_images=max(n, 8)) as e:
+        for _ in range(3):
+            e.encode(images)
+        ts = []
+        for _ in range(iters):
+            e.encode(images)
+            ts.append(e.last_device_ms)
+    p50 = float(np.median(ts))
+    return {"images": n, "image_hw": list(spec.image_hw), "crop_hw": list(spec.crop_hw),
+            "keypoints": spec.keypoints, "device_p50_ms": round(p50, 4),
+            "us_per_image": round(p50 * 1e3 / n, 2),
+            "definition": "fe_encoder_encode on host images; device time of the encoder's graph "
+                          "(hipEvents), synthetic LeRobot-named weights"}
+
+
 def dominant_roofline(eng, iters: int):
     """Live measurement of the dominant convolution (hipEvents around `iters` rounds)."""
     convs = [c for c in eng.convolutions() if shape_of(c["name"]) == DOMINANT_SHAPE]
@@ -349,6 +374,8 @@ def main():
                     help="rounds over the dominant convolution's layers")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel loop and a 256 MiB calibration copy")
+    ap.add_argument("--encoder", type=int, metavar="IMAGES",
+                    help="only the observation encoder on that many camera images, as JSON")
     ap.add_argument("--breakdown", metavar="WORKLOAD:BATCH",
                     help="only the per-shape convolution timing of one U-Net evaluation at that "
                          "batch (diagnostics and profiling), as JSON")
@@ -364,6 +391,11 @@ def main():
 
     import flowedge_amd
     from flowedge_amd import checkpoint as ck
+
+    if args.encoder:
+        print(json.dumps({"observation_encoder": encoder_timing(args.encoder, iters=100)}),
+              flush=True)
+        return
 
     if args.breakdown:
         work, batch = args.breakdown.split(":")
@@ -605,6 +637,7 @@ def main():
     }
     if not args.no_extra:
         result["other_configs"] = extra_configs(check=not args.no_cpu)
+        result["observation_encoder"] = encoder_timing(2)
     if not args.no_cpu:
         cpu = cpu_baseline(path, spec, args.cpu_budget)
         result["cpu_baseline"] = {
