@@ -583,6 +583,15 @@ int conv_mfma_parts(const ConvOp& op, int split, std::int64_t src_stride, const 
       .ksplit;
 }
 
+int conv_mfma_ksplit(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
+                     std::int64_t plain_stride, int batch, std::size_t workspace_floats,
+                     bool bf16_mma, bool f32_split, int max_parts) {
+  if (!conv_mfma_supported(op, split) || batch <= 0) return 1;
+  return mm_plan(op, split, src_stride, plain, plain_stride, batch, workspace_floats, bf16_mma,
+                 f32_split, max_parts)
+      .ksplit;
+}
+
 hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride, int split,
                      const float* plain, std::int64_t plain_stride, View y, int batch,
                      float* workspace, std::size_t workspace_floats, bool bf16_mma,

@@ -57,6 +57,10 @@ constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
 constexpr std::size_t kSplitKFloats = 1024 * 64 * 128;  // split-K partials: <= 1024 tiles of 64 x 128
 // Largest batch whose convolutions run input-channel sliced (on the fused kernels; the matrix
 // cores take over from 5 samples with F32 weights, 8 with BF16 weights).
+// Smallest reduction length (input channels x taps) of a convolution whose 1x1 projection is
+// forked to the side stream.
+constexpr int kForkMinReduction = 1024;
+
 constexpr std::size_t kSliceBatch = 8;
 // Largest batch whose matrix-core convolutions leave the partial sums of a split K loop in the
 // output tensor for their consumers to add (larger batches split K rarely; those that do reduce
@@ -248,6 +252,10 @@ struct FeEngine {
   hipError_t scratch_status = hipErrorNotInitialized;
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // Side stream for a matrix-core convolution's 1x1 projection, forked from and joined back to
+  // `stream` (in a captured graph: two parallel nodes).
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
   float last_ms = -1.0f;
   bool timed = false;
 
@@ -366,6 +374,9 @@ struct FeEngine {
       if (g) (void)hipGraphExecDestroy(g);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
+    if (fork) (void)hipEventDestroy(fork);
+    if (join) (void)hipEventDestroy(join);
+    if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamDestroy(stream);
     if (arena) (void)hipFree(arena);
     if (pin_cond) (void)hipHostFree(pin_cond);
@@ -890,11 +901,34 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     }
     float* ws = e.wp(e.w.splitk);
     const std::size_t wsf = e.w.splitk_floats;
+    const int mp = slices.matrix ? slices.slices : 0;
+    const int mpr = slices.matrix ? slices.res_slices : 0;
+    if (res != nullptr && e.side != nullptr && op.ic * op.k >= kForkMinReduction &&
+        conv_mfma_ksplit(op, in.split, ss, in.plain, in.plain_stride, batch, wsf, e.bf16_mma,
+                         e.f32_split, mp) == 1 &&
+        conv_mfma_ksplit(*res, in.split, ss, in.plain, in.plain_stride, batch, wsf, e.bf16_mma,
+                         e.f32_split, mpr) == 1) {
+      // Batches large enough that neither GEMM splits its K loop, and a reduction long enough
+      // to pay for the fork: the 1x1 projection reads the same staged input as the convolution
+      // and writes its own output, so it runs on the side stream, forked after the prologue
+      // and joined before the next layer, and fills the CUs the convolution's last wave of
+      // tiles leaves idle.  A fork and join costs tens of microseconds of graph
+      // synchronization: at batches that split K, or on the 2- or 14-channel input layer, it
+      // costs more than the overlap gains (bimanual B=64 6.32 -> 6.82 ms).
+      FE_TRY(hipEventRecord(e.fork, s));
+      FE_TRY(hipStreamWaitEvent(e.side, e.fork, 0));
+      FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws, wsf,
+                       e.bf16_mma, e.f32_split, e.side, mpr));
+      FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws, wsf,
+                       e.bf16_mma, e.f32_split, s, mp));
+      FE_TRY(hipEventRecord(e.join, e.side));
+      return hipStreamWaitEvent(s, e.join, 0);
+    }
     FE_TRY(conv_mfma(op, src, ss, in.split, in.plain, in.plain_stride, y, batch, ws, wsf,
-                     e.bf16_mma, e.f32_split, s, slices.matrix ? slices.slices : 0));
+                     e.bf16_mma, e.f32_split, s, mp));
     if (res != nullptr)
       FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws, wsf,
-                       e.bf16_mma, e.f32_split, s, slices.matrix ? slices.res_slices : 0));
+                       e.bf16_mma, e.f32_split, s, mpr));
     return hipSuccess;
   }
   return conv_fused(op, res, in, y, yr, batch, s);
@@ -1965,6 +1999,12 @@ std::size_t env_mfma_batch() {
   return (end && *end == '\0') ? n : 0;
 }
 
+// FLOWEDGE_SIDE_STREAM=0 keeps every matrix-core projection on the engine stream.
+bool side_streams() {
+  const char* v = std::getenv("FLOWEDGE_SIDE_STREAM");
+  return v == nullptr || std::strcmp(v, "0") != 0;
+}
+
 std::size_t env_max_batch() {
   const char* v = std::getenv("FLOWEDGE_MAX_BATCH");
   if (v == nullptr || *v == '\0') return 256;
@@ -2139,7 +2179,11 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   e->pin_status = reinterpret_cast<unsigned*>(e->pin_seed + 1);
   *e->pin_status = 0;
   if ((st = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
-      (st = hipEventCreate(&e->ev0)) != hipSuccess || (st = hipEventCreate(&e->ev1)) != hipSuccess) {
+      (st = hipEventCreate(&e->ev0)) != hipSuccess || (st = hipEventCreate(&e->ev1)) != hipSuccess ||
+      (side_streams() &&
+       ((st = hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking)) != hipSuccess ||
+        (st = hipEventCreateWithFlags(&e->fork, hipEventDisableTiming)) != hipSuccess ||
+        (st = hipEventCreateWithFlags(&e->join, hipEventDisableTiming)) != hipSuccess))) {
     hip_fail("Stream creation failed", st);
     return nullptr;
   }

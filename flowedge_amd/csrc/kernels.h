@@ -128,6 +128,10 @@ hipError_t conv_mfma(const ConvOp& op, const float* src, std::int64_t src_stride
 int conv_mfma_parts(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
                     std::int64_t plain_stride, int batch, bool bf16_mma, bool f32_split,
                     int max_parts);
+// The K split conv_mfma runs with these arguments (1: none).
+int conv_mfma_ksplit(const ConvOp& op, int split, std::int64_t src_stride, const float* plain,
+                     std::int64_t plain_stride, int batch, std::size_t workspace_floats,
+                     bool bf16_mma, bool f32_split, int max_parts);
 // dst[b][0 : n) = sum over p < parts of src[b * src_stride + p * part_stride + ...), added in
 // order: the plain input of a matrix-core convolution whose producer left partial sums.
 hipError_t sum_parts(const float* src, std::int64_t src_stride, int parts,
