@@ -57,9 +57,9 @@ constexpr std::size_t kMaxStages = 8;    // diffusion.h:41
 constexpr std::size_t kSplitKFloats = 1024 * 64 * 128;  // split-K partials: <= 1024 tiles of 64 x 128
 // Largest batch whose convolutions run input-channel sliced (on the fused kernels; the matrix
 // cores take over from 5 samples with F32 weights, 8 with BF16 weights).
-// Smallest reduction length (input channels x taps) of a convolution whose 1x1 projection is
-// forked to the side stream.
-constexpr int kForkMinReduction = 1024;
+// Smallest convolution (multiply-adds x 2, whole batch) whose 1x1 projection is forked to the
+// side stream: the fork and join cost tens of microseconds of graph synchronization.
+constexpr double kForkMinFlops = 2e10;
 
 constexpr std::size_t kSliceBatch = 8;
 // Largest batch whose matrix-core convolutions leave the partial sums of a split K loop in the
@@ -903,18 +903,18 @@ hipError_t dispatch_conv(FeEngine& e, const fe::hip::ConvOp& op, const fe::hip::
     const std::size_t wsf = e.w.splitk_floats;
     const int mp = slices.matrix ? slices.slices : 0;
     const int mpr = slices.matrix ? slices.res_slices : 0;
-    if (res != nullptr && e.side != nullptr && op.ic * op.k >= kForkMinReduction &&
+    if (res != nullptr && e.side != nullptr &&
+        2.0 * op.oc * op.ic * op.k * op.lout * batch >= kForkMinFlops &&
         conv_mfma_ksplit(op, in.split, ss, in.plain, in.plain_stride, batch, wsf, e.bf16_mma,
                          e.f32_split, mp) == 1 &&
         conv_mfma_ksplit(*res, in.split, ss, in.plain, in.plain_stride, batch, wsf, e.bf16_mma,
                          e.f32_split, mpr) == 1) {
-      // Batches large enough that neither GEMM splits its K loop, and a reduction long enough
-      // to pay for the fork: the 1x1 projection reads the same staged input as the convolution
-      // and writes its own output, so it runs on the side stream, forked after the prologue
-      // and joined before the next layer, and fills the CUs the convolution's last wave of
-      // tiles leaves idle.  A fork and join costs tens of microseconds of graph
-      // synchronization: at batches that split K, or on the 2- or 14-channel input layer, it
-      // costs more than the overlap gains (bimanual B=64 6.32 -> 6.82 ms).
+      // Convolutions large enough to pay for a fork (about 20 GFLOP and up) whose GEMMs need
+      // no K split: the 1x1 projection reads the same staged input as the convolution and
+      // writes its own output, so it runs on the side stream, forked after the prologue and
+      // joined before the next layer, and fills the CUs the convolution's last wave of tiles
+      // leaves idle.  Smaller ones lose to the fork's synchronization (bimanual B=64 6.32 ->
+      // 6.82 ms with every projection forked, pusht B=128 +0.3%).
       FE_TRY(hipEventRecord(e.fork, s));
       FE_TRY(hipStreamWaitEvent(e.side, e.fork, 0));
       FE_TRY(conv_mfma(*res, src, ss, in.split, in.plain, in.plain_stride, yr, batch, ws, wsf,
