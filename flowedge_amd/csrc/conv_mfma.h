@@ -77,15 +77,18 @@ __device__ __forceinline__ int src_at(int t, int k) {
   }
 }
 
-// BF16 matrix-core path: the K loop walks 32 input channels per step.
+// BF16 matrix-core path: each MFMA contracts kKCB input channels of one tap; a K step stages
+// kKCB channels (F32 weights, split while staged) or 2 kKCB (BF16 weights).
 constexpr int kKCB = 32;
+inline int mm_bf16_step(const ConvOp& op) { return op.bf16 ? 2 * kKCB : kKCB; }
 
-// True when the BF16 kernels cover this convolution's shape (32-channel multiples).
+// True when the BF16 kernels cover this convolution's shape (input channels and the concat
+// split in multiples of the K step).
 bool mm_bf16_ok(const ConvOp& op, int split);
 
-// Launches the BF16 implicit GEMM for `a` (tiles and split as the F32 path plans them, with K
-// steps of kKCB channels): two BF16 terms of the input against BF16 weights, or three products
-// of split input and split F32 weights.
+// Launches the BF16 implicit GEMM for `a` (tiles and split as the F32 path plans them): two BF16
+// terms of the input against BF16 weights, or three products of split input and split F32
+// weights.
 hipError_t launch_mm_bf16(const ConvOp& op, int tile, const MmArgs& a, hipStream_t s);
 
 }  // namespace fe::hip::mm

@@ -552,7 +552,7 @@ MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float
     p.ntiles = (batch + 32 / op.lout - 1) / (32 / op.lout);
   }
   const int tiles = p.mtiles * p.ntiles;
-  const int nsteps = p.use_bf16 ? op.ic / kKCB : (op.ic + kKC - 1) / kKC;
+  const int nsteps = p.use_bf16 ? op.ic / mm_bf16_step(op) : (op.ic + kKC - 1) / kKC;
   // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
   // workgroups per CU, so that two K steps of weights stream per CU at a time.
   if (tiles < tune.target / 2) {

@@ -12,8 +12,12 @@
 //
 // Lane layouts (checked on gfx950): a lane holds A[l % 16][8 (l / 16) .. +7] and
 // B[8 (l / 16) .. +7][l % 16] as eight BF16 values, and receives D[4 (l / 16) + e][l % 16].
-// In LDS a weight row stores the 32 channels of each tap contiguously and an input row (one
-// sample position) its 32 channels, so every operand is one 16-byte read.
+// In LDS a weight row stores the KS channels of each tap contiguously and an input row (one
+// sample position) its KS channels, so every operand is one 16-byte read.  A K step stages KS =
+// 64 channels with BF16 weights (two contractions per tap; one weight buffer, refilled after a
+// barrier, so that two 79 KB workgroups fit a CU) and 32 with F32 weights (double-buffered):
+// half the steps, and so half the per-step staging chains, of 32-channel steps at BF16
+// (bimanual B=16 4.87 -> 4.72 ms).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -40,14 +44,18 @@ struct BShape {
   static constexpr int kWaveCols = kBThreads / 64 / kWaveRows;
   static constexpr int LOUT = lout_for(MODE, LIN);
   static constexpr int SB = NT / LOUT;            // samples per column tile
-  static constexpr int WROW = K * kKCB + kPadB;   // LDS BF16 values per weight row
-  static constexpr int XROW = kKCB + kPadB;       // LDS BF16 values per (sample, position) row
+  static constexpr int KS = WF32 ? kKCB : 2 * kKCB;  // input channels per K step (mm_bf16_step)
+  static constexpr int SUB = KS / kKCB;              // MFMA contractions per tap and step
+  static constexpr bool W1 = !WF32;                  // one weight buffer in LDS
+  static constexpr int WBUF = W1 ? 1 : 2;
+  static constexpr int WROW = K * KS + kPadB;   // LDS BF16 values per weight row
+  static constexpr int XROW = KS + kPadB;       // LDS BF16 values per (sample, position) row
   static constexpr int ZERO = SB * LIN;           // index of the zero row
   static constexpr int XROWS = SB * LIN + 1;
   static constexpr int WVALS = MT * WROW;
   static constexpr int XVALS = XROWS * XROW;
   // 16-byte weight units per lane per step: 8 BF16 values, or 4 F32 values.
-  static constexpr int WUNITS = MT * K * (kKCB / (WF32 ? 4 : 8));  // weight units per step
+  static constexpr int WUNITS = MT * K * (KS / (WF32 ? 4 : 8));  // weight units per step
   static constexpr int UW = (WUNITS + kBThreads - 1) / kBThreads;
   static constexpr int WARR = WF32 ? 2 : 1;  // weight arrays in LDS (hi, lo)
   // Input units: CPU channels x PPU positions of one sample, read as contiguous 16-byte vectors
@@ -56,11 +64,11 @@ struct BShape {
   static constexpr int CPU = LIN == 1 ? 4 : 2;
   static constexpr int PPU = LIN >= 4 ? 4 : LIN;
   static constexpr int XVEC = LIN >= 4 ? 2 : 1;     // 16-byte loads per unit
-  static constexpr int UPS = (kKCB / CPU) * (LIN / PPU);  // units per sample and step
+  static constexpr int UPS = (KS / CPU) * (LIN / PPU);  // units per sample and step
   static constexpr int XUNITS = SB * UPS;
   static constexpr int WM = MT / kWaveRows, WN = NT / kWaveCols;
   static constexpr int TI = WM / 16, TJ = WN / 16;
-  static constexpr std::size_t LDS_BYTES = (2 * WARR * WVALS + 4 * XVALS) * 2;
+  static constexpr std::size_t LDS_BYTES = (WBUF * WARR * WVALS + 4 * XVALS) * 2;
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wavefront tiles of 16 x 16 MFMA blocks");
   static_assert(NT % LOUT == 0, "column tile");
   static constexpr int UXN = (XUNITS + kBThreads - 1) / kBThreads;  // input units per lane
@@ -91,8 +99,8 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   constexpr int kBThreads = S::kBThreads, kWaveCols = S::kWaveCols;
   extern __shared__ uint4 lds_b[];
   unsigned short* Ws = reinterpret_cast<unsigned short*>(lds_b);  // [2][WVALS] (hi)
-  unsigned short* Wl = Ws + 2 * S::WVALS;                          // [2][WVALS] (lo, F32 weights)
-  unsigned short* Xh = Ws + 2 * S::WARR * S::WVALS;                // [2][XVALS]
+  unsigned short* Wl = Ws + S::WBUF * S::WVALS;                    // [2][WVALS] (lo, F32 weights)
+  unsigned short* Xh = Ws + S::WBUF * S::WARR * S::WVALS;          // [2][XVALS]
   unsigned short* Xl = Xh + 2 * S::XVALS;                          // [2][XVALS]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -106,12 +114,12 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   const int mt = tile / a.ntiles, nt = tile - mt * a.ntiles;
   const int m0 = mt * MT;
   const int b0 = nt * S::SB;
-  const int nall = a.ic / kKCB;
+  const int nall = a.ic / S::KS;
   const int s0 = ks * nall / a.ksplit, s1 = (ks + 1) * nall / a.ksplit;
 
   // Zero rows of both input buffers (never overwritten).
-  if (tid < 2 * kKCB) {
-    const int buf = tid / kKCB, c = tid % kKCB;
+  if (tid < 2 * S::KS) {
+    const int buf = tid / S::KS, c = tid % S::KS;
     Xh[buf * S::XVALS + S::ZERO * S::XROW + c] = 0;
     Xl[buf * S::XVALS + S::ZERO * S::XROW + c] = 0;
   }
@@ -119,7 +127,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   // Staging.  Every global read is a buffer load whose per-lane byte offset is fixed for the
   // whole K loop (computed once below); a wave-uniform scalar offset walks the K steps, and lanes
   // with nothing to read get an out-of-range offset, which returns zeros without a branch.
-  constexpr int QPT = kKCB / (WF32 ? 4 : 8);  // 16-byte weight units per (row, tap)
+  constexpr int QPT = S::KS / (WF32 ? 4 : 8);  // 16-byte weight units per (row, tap)
   constexpr int QW = WF32 ? 4 : 8;             // weights per unit
   constexpr unsigned ES = WF32 ? 4u : 2u;      // weight element size
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(a.w, a.wbytes);
@@ -135,7 +143,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     const int oc = m0 + m;
     wvoff[r] = act && oc < a.oc ? static_cast<unsigned>((oc * K + k) * a.ic + QW * q) * ES
                                 : kOutOfRange;
-    wlds[r] = act ? m * S::WROW + k * kKCB + QW * q : -1;
+    wlds[r] = act ? m * S::WROW + k * S::KS + QW * q : -1;
   }
   // Input units (see BShape): consecutive lanes read consecutive 16-byte pieces of a sample's
   // 32-channel block, and each unit is stored as PPU rows (positions) of CPU BF16 channels per
@@ -169,7 +177,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     float4 x[S::UXN][S::XVEC];
   };
   auto load_step = [&](int step, Regs& R) {
-    const int ic0 = step * kKCB;
+    const int ic0 = step * S::KS;
     const unsigned ws = static_cast<unsigned>(ic0) * ES;
 #pragma unroll
     for (int r = 0; r < S::UW; ++r)
@@ -188,7 +196,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     }
   };
   auto store_step = [&](int buf, const Regs& R) {
-    unsigned short* W = Ws + buf * S::WVALS;
+    unsigned short* W = Ws + (S::W1 ? 0 : buf * S::WVALS);
 #pragma unroll
     for (int r = 0; r < S::UW; ++r) {
       if (S::WUNITS % kBThreads != 0 && wlds[r] < 0) continue;
@@ -269,7 +277,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     for (int j = 0; j < S::TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](int buf) {
-    const unsigned short* W = Ws + buf * S::WVALS;
+    const unsigned short* W = Ws + (S::W1 ? 0 : buf * S::WVALS);
     const unsigned short* WL = Wl + buf * S::WVALS;
     const unsigned short* H = Xh + buf * S::XVALS;
     const unsigned short* L = Xl + buf * S::XVALS;
@@ -279,29 +287,34 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
       if constexpr (PAR) {
         if (((k + par + 1) & 1) != 0) continue;
       }
-      bf16x8 av[S::TI], al[WF32 ? S::TI : 1], bh[S::TJ], bl[S::TJ];
 #pragma unroll
-      for (int i = 0; i < S::TI; ++i) {
-        av[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
-                                               W + arow + i * 16 * S::WROW + k * kKCB));
-        if constexpr (WF32)
-          al[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
-                                                 WL + arow + i * 16 * S::WROW + k * kKCB));
-      }
+      for (int kc = 0; kc < S::SUB; ++kc) {
+        bf16x8 av[S::TI], al[WF32 ? S::TI : 1], bh[S::TJ], bl[S::TJ];
+        const int wo = k * S::KS + kc * kKCB;
 #pragma unroll
-      for (int j = 0; j < S::TJ; ++j) {
-        bh[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(H + xrow[j][k]));
-        bl[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(L + xrow[j][k]));
-      }
-#pragma unroll
-      for (int i = 0; i < S::TI; ++i)
+        for (int i = 0; i < S::TI; ++i) {
+          av[i] = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const uint4*>(W + arow + i * 16 * S::WROW + wo));
+          if constexpr (WF32)
+            al[i] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const uint4*>(WL + arow + i * 16 * S::WROW + wo));
+        }
 #pragma unroll
         for (int j = 0; j < S::TJ; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bh[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bl[j], acc[i][j], 0, 0, 0);
-          if constexpr (WF32)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+          const int xo = xrow[j][k] + kc * kKCB;
+          bh[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(H + xo));
+          bl[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(L + xo));
         }
+#pragma unroll
+        for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+          for (int j = 0; j < S::TJ; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bh[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bl[j], acc[i][j], 0, 0, 0);
+            if constexpr (WF32)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+          }
+      }
     }
   };
 
@@ -316,7 +329,10 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     const int buf = (step - s0) & 1;
     if (step + 1 < s1) load_step(step + 1, rn);
     compute(buf);
-    if (step + 1 < s1) store_step(buf ^ 1, rn);
+    if (step + 1 < s1) {
+      if constexpr (S::W1) __syncthreads();  // the one weight buffer is read by every wavefront
+      store_step(buf ^ 1, rn);
+    }
     __syncthreads();
   }
 
@@ -409,7 +425,8 @@ hipError_t by_lin(int lin, int tile, bool wf32, const MmArgs& a, hipStream_t s) 
 }  // namespace
 
 bool mm_bf16_ok(const ConvOp& op, int split) {
-  if (op.ic % kKCB != 0 || split % kKCB != 0 || split <= 0 || split > op.ic) return false;
+  const int ks = mm_bf16_step(op);
+  if (op.ic % ks != 0 || split % ks != 0 || split <= 0 || split > op.ic) return false;
   if (op.lin != 1 && op.lin != 2 && op.lin != 4 && op.lin != 8 && op.lin != 16) return false;
   if (op.lout != lout_for(op.mode, op.lin)) return false;
   if (op.mode == kConvSame) return op.k == 1 || op.k == 3 || op.k == 5;
