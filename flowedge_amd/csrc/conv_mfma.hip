@@ -38,24 +38,29 @@ using namespace mm;
 constexpr int kKC = 16;   // input channels per K step
 constexpr int kPad = 4;   // LDS row padding (floats)
 
-template <int MODE, int K, int LIN, int MT, int NT>
+// KS: input channels per K step, kKC (narrow inputs, double-buffered weights) or 2 kKC (one
+// weight buffer, refilled after a barrier: half the per-step staging chains).
+template <int MODE, int K, int LIN, int MT, int NT, int KS = kKC>
 struct MmShape {
   static constexpr int LOUT = lout_for(MODE, LIN);
   static constexpr int SB = NT / LOUT;           // samples per column tile
-  static constexpr int WROW = K * kKC + kPad;    // LDS floats per weight row
-  static constexpr int XROW = kKC + kPad;        // LDS floats per (sample, position) row
+  static constexpr bool W1 = KS > kKC;           // one weight buffer in LDS
+  static constexpr int WBUF = W1 ? 1 : 2;
+  static constexpr int WROW = K * KS + kPad;     // LDS floats per weight row
+  static constexpr int XROW = KS + kPad;         // LDS floats per (sample, position) row
   static constexpr int ZERO = SB * LIN;          // index of the zero row
   static constexpr int XROWS = SB * LIN + 1;
   static constexpr int WFLOATS = MT * WROW;
   static constexpr int XFLOATS = XROWS * XROW;
-  static constexpr int UW = MT * K * 4 / kMmThreads;  // weight float4 per lane per step
-  static constexpr int XELEMS = SB * kKC * LIN;       // input floats per step
+  static constexpr int UW = MT * K * (KS / 4) / kMmThreads;  // weight float4 per lane per step
+  static constexpr int XELEMS = SB * KS * LIN;               // input floats per step
   static constexpr int XV = LIN >= 4 ? 4 : 1;          // vector width of input loads
   static constexpr int XUNITS = XELEMS / XV;
   static constexpr int UX = (XUNITS + kMmThreads - 1) / kMmThreads;
   static constexpr int WM = MT / 2, WN = NT / 2;
   static constexpr int TI = WM / 16, TJ = WN / 16;
-  static_assert(MT * K * 4 % kMmThreads == 0, "weight units per lane");
+  static_assert(MT * K * (KS / 4) % kMmThreads == 0, "weight units per lane");
+  static constexpr std::size_t LDS_FLOATS = WBUF * WFLOATS + 2 * XFLOATS;
   static_assert(NT % LOUT == 0 && XELEMS % XV == 0, "column tile");
 };
 
@@ -72,10 +77,11 @@ __device__ __forceinline__ float4 load_w4(const void* base, std::int64_t idx) {
 
 template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
 __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
-  using S = MmShape<MODE, K, LIN, MT, NT>;
+  using S = MmShape<MODE, K, LIN, MT, NT, NARROW ? kKC : 2 * kKC>;
+  constexpr int KS = NARROW ? kKC : 2 * kKC;
   extern __shared__ float4 lds4[];
-  float* Ws = reinterpret_cast<float*>(lds4);  // [2][WFLOATS]
-  float* Xs = Ws + 2 * S::WFLOATS;             // [2][XFLOATS]
+  float* Ws = reinterpret_cast<float*>(lds4);  // [WBUF][WFLOATS]
+  float* Xs = Ws + S::WBUF * S::WFLOATS;       // [2][XFLOATS]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -90,22 +96,22 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   const int mt = tile / a.ntiles, nt = tile - mt * a.ntiles;
   const int m0 = mt * MT;
   const int b0 = nt * S::SB;
-  const int nall = (a.ic + kKC - 1) / kKC;
+  const int nall = (a.ic + KS - 1) / KS;
   const int s0 = ks * nall / a.ksplit, s1 = (ks + 1) * nall / a.ksplit;
 
   // Zero rows of both input buffers (never overwritten).
-  if (tid < 2 * kKC) Xs[(tid / kKC) * S::XFLOATS + S::ZERO * S::XROW + (tid % kKC)] = 0.0f;
+  if (tid < 2 * KS) Xs[(tid / KS) * S::XFLOATS + S::ZERO * S::XROW + (tid % KS)] = 0.0f;
 
   float4 wreg[S::UW];
   float4 xreg[S::UX > 0 ? S::UX : 1];
   float xs1[S::XV == 1 ? S::UX : 1];
   auto load_step = [&](int step) {
-    const int ic0 = step * kKC;
+    const int ic0 = step * KS;
 #pragma unroll
     for (int r = 0; r < S::UW; ++r) {
       const int u = tid + r * kMmThreads;
-      const int m = u / (K * 4), rem = u - m * (K * 4);
-      const int k = rem >> 2, q = rem & 3;
+      const int m = u / (K * (KS / 4)), rem = u - m * (K * (KS / 4));
+      const int k = rem / (KS / 4), q = rem % (KS / 4);
       const int oc = m0 + m;
       if constexpr (NARROW) {
         // Channel counts that are not a multiple of 16: element-wise guarded loads.
@@ -130,7 +136,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     for (int r = 0; r < S::UX; ++r) {
       const int u = tid + r * kMmThreads;
       if constexpr (S::XV == 4) {
-        const int bl = u / (4 * LIN), v = u - bl * (4 * LIN);
+        const int bl = u / (KS / 4 * LIN), v = u - bl * (KS / 4 * LIN);
         const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
         const int b = b0 + bl, c = ic0 + ch;
         float4 val = float4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
         }
         xreg[r] = val;
       } else {
-        const int bl = u / (kKC * LIN), v = u - bl * (kKC * LIN);
+        const int bl = u / (KS * LIN), v = u - bl * (KS * LIN);
         const int ch = v / LIN, t = v - ch * LIN;
         const int b = b0 + bl, c = ic0 + ch;
         float val = 0.0f;
@@ -154,21 +160,21 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     }
   };
   auto store_step = [&](int buf) {
-    float* W = Ws + buf * S::WFLOATS;
+    float* W = Ws + (S::W1 ? 0 : buf * S::WFLOATS);
     float* X = Xs + buf * S::XFLOATS;
 #pragma unroll
     for (int r = 0; r < S::UW; ++r) {
       const int u = tid + r * kMmThreads;
-      const int m = u / (K * 4), rem = u - m * (K * 4);
-      const int k = rem >> 2, q = rem & 3;
-      *reinterpret_cast<float4*>(W + m * S::WROW + k * kKC + 4 * q) = wreg[r];
+      const int m = u / (K * (KS / 4)), rem = u - m * (K * (KS / 4));
+      const int k = rem / (KS / 4), q = rem % (KS / 4);
+      *reinterpret_cast<float4*>(W + m * S::WROW + k * KS + 4 * q) = wreg[r];
     }
 #pragma unroll
     for (int r = 0; r < S::UX; ++r) {
       const int u = tid + r * kMmThreads;
       if (u >= S::XUNITS) continue;
       if constexpr (S::XV == 4) {
-        const int bl = u / (4 * LIN), v = u - bl * (4 * LIN);
+        const int bl = u / (KS / 4 * LIN), v = u - bl * (KS / 4 * LIN);
         const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
         float* row = X + (bl * LIN + t4) * S::XROW + ch;
         row[0] = xreg[r].x;
@@ -176,7 +182,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
         row[2 * S::XROW] = xreg[r].z;
         row[3 * S::XROW] = xreg[r].w;
       } else {
-        const int bl = u / (kKC * LIN), v = u - bl * (kKC * LIN);
+        const int bl = u / (KS * LIN), v = u - bl * (KS * LIN);
         const int ch = v / LIN, t = v - ch * LIN;
         X[(bl * LIN + t) * S::XROW + ch] = xs1[r];
       }
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   for (int step = s0; step < s1; ++step) {
     const int buf = (step - s0) & 1;
     if (step + 1 < s1) load_step(step + 1);
-    const float* W = Ws + buf * S::WFLOATS;
+    const float* W = Ws + (S::W1 ? 0 : buf * S::WFLOATS);
     const float* X = Xs + buf * S::XFLOATS;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -223,23 +229,31 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
       if constexpr (PAR) {
         if (((k + wc + 1) & 1) != 0) continue;
       }
-      float4 av[S::TI], bv[S::TJ];
 #pragma unroll
-      for (int i = 0; i < S::TI; ++i)
-        av[i] = *reinterpret_cast<const float4*>(W + arow + i * 16 * S::WROW + k * kKC);
+      for (int kc = 0; kc < KS / kKC; ++kc) {
+        float4 av[S::TI], bv[S::TJ];
 #pragma unroll
-      for (int j = 0; j < S::TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(X + xrow[j][k]);
+        for (int i = 0; i < S::TI; ++i)
+          av[i] = *reinterpret_cast<const float4*>(W + arow + i * 16 * S::WROW + k * KS +
+                                                   kc * kKC);
 #pragma unroll
-      for (int i = 0; i < S::TI; ++i)
+        for (int j = 0; j < S::TJ; ++j)
+          bv[j] = *reinterpret_cast<const float4*>(X + xrow[j][k] + kc * kKC);
 #pragma unroll
-        for (int j = 0; j < S::TJ; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
-        }
+        for (int i = 0; i < S::TI; ++i)
+#pragma unroll
+          for (int j = 0; j < S::TJ; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
+          }
+      }
     }
-    if (step + 1 < s1) store_step(buf ^ 1);
+    if (step + 1 < s1) {
+      if constexpr (S::W1) __syncthreads();  // the one weight buffer is read by every wavefront
+      store_step(buf ^ 1);
+    }
     __syncthreads();
   }
 
@@ -259,7 +273,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   // [channel], so that each sample's MT x LOUT block (contiguous in y) is written by
   // consecutive lanes.
   constexpr int TROW = MT + 1;
-  if constexpr (NT * TROW <= 2 * (S::WFLOATS + S::XFLOATS)) {
+  if constexpr (NT * TROW <= S::LDS_FLOATS) {
     float* T = reinterpret_cast<float*>(lds4);
     __syncthreads();  // the last K step's LDS reads are done
 #pragma unroll
@@ -409,8 +423,8 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
 
 template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
 hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
-  using S = MmShape<MODE, K, LIN, MT, NT>;
-  const std::size_t smem = (2 * S::WFLOATS + 2 * S::XFLOATS) * sizeof(float);
+  using S = MmShape<MODE, K, LIN, MT, NT, NARROW ? kKC : 2 * kKC>;
+  const std::size_t smem = S::LDS_FLOATS * sizeof(float);
   auto fn = conv_mfma_kernel<MODE, K, LIN, BF16, MT, NT, NARROW>;
   static bool raised = false;
   if (!raised && smem > 48 * 1024) {
@@ -480,8 +494,9 @@ bool lin_mm_ok(int mode, int lin) {
 bool conv_mfma_supported(const ConvOp& op, int split) {
   if (!lin_mm_ok(op.mode, op.lin) || op.lout != lout_for(op.mode, op.lin)) return false;
   if (split > op.ic || split <= 0 || op.oc <= 0 || op.ic <= 0) return false;
-  if (op.ic % kKC != 0) {
-    // Narrow inputs (the first convolution reads action_dim channels): one plain source.
+  if (op.ic % (2 * kKC) != 0) {
+    // Narrow inputs (the first convolution reads action_dim channels; widths that are not
+    // 32-channel multiples): one plain source, 16-channel steps with guarded loads.
     return split == op.ic && op.mode == kConvSame && (op.k == 1 || op.k == 3 || op.k == 5);
   }
   if (split % kKC != 0) return false;
@@ -526,7 +541,7 @@ MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float
                bool f32_split, int max_parts) {
   const MmTuning& tune = mm_tuning();
   MmPlan p;
-  p.narrow = op.ic % kKC != 0;
+  p.narrow = op.ic % (2 * kKC) != 0;
   p.mtiles = (op.oc + 63) / 64;
   p.ntiles = (batch + 128 / op.lout - 1) / (128 / op.lout);
   const bool small = tune.tile == 64 || (tune.tile != 128 && p.mtiles * p.ntiles < 256);
@@ -552,7 +567,8 @@ MmPlan mm_plan(const ConvOp& op, int split, std::int64_t src_stride, const float
     p.ntiles = (batch + 32 / op.lout - 1) / (32 / op.lout);
   }
   const int tiles = p.mtiles * p.ntiles;
-  const int nsteps = p.use_bf16 ? op.ic / mm_bf16_step(op) : (op.ic + kKC - 1) / kKC;
+  const int fks = p.narrow ? kKC : 2 * kKC;  // F32 kernel's K step
+  const int nsteps = p.use_bf16 ? op.ic / mm_bf16_step(op) : (op.ic + fks - 1) / fks;
   // Split the K loop when the output tiles alone leave CUs idle (small batches): aim at two
   // workgroups per CU, so that two K steps of weights stream per CU at a time.
   if (tiles < tune.target / 2) {
