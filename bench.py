@@ -241,13 +241,13 @@ def extra_configs(iters: int = 10, check: bool = True):
             row["max_abs_err_vs_oracle"] = oracle_check(ck.cached_checkpoint(work), cond, noise,
                                                         do.cpu().numpy(), steps, idx, kind, mode)
             row["oracle_samples"] = idx
-        # The engine's default matrix-core thresholds: 5 samples (F32 weights), 8 (BF16).
-        if batch >= 8 and spec.bf16_weights:
+        # The engine's default matrix-core thresholds: 4 samples (F32 weights), 5 (BF16).
+        if batch >= 5 and spec.bf16_weights:
             # BF16 weights on the BF16 matrix cores, input split in two terms: two MFMA
             # products per useful product.
             row["mfma"] = "bf16 (2 products per multiply)"
             row["mfma_frac"] = round(2 * tflops / BF16_MFMA_PEAK_TFLOPS, 4)
-        elif batch >= 5 and not spec.bf16_weights:
+        elif batch >= 4 and not spec.bf16_weights:
             row["mfma"] = "fp32"
             row["mfma_frac"] = round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)
         rows.append(row)

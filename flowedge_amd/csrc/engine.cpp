@@ -289,7 +289,7 @@ struct FeEngine {
   };
   std::size_t flow_pool = 0, flow_pool_rows = 0, flow_pool_used = 0;
   std::vector<FlowTable> flow_tables;
-  std::size_t mfma_batch = 5;  // batches of at least this many samples use the matrix cores
+  std::size_t mfma_batch = 4;  // batches of at least this many samples use the matrix cores
   // Input-channel slicing of the fused convolutions (batches below mfma_batch, up to the Work's
   // slice_batch): on when every convolution of the model runs fused and the final update sums
   // partials; slice_max (FLOWEDGE_SLICES, default kMaxSlices; 1 turns slicing off) caps it.
@@ -1988,9 +1988,10 @@ std::uint64_t nfe_for(std::size_t steps, int kind, int mode) {
 }
 
 // Smallest batch that runs the convolutions on the matrix cores (FLOWEDGE_MFMA_BATCH; 0 = by
-// weight type: 5 samples for F32 convolutions, 8 for BF16, where streaming half the bytes keeps
-// the batch-1 kernels ahead longer; a value above the max batch keeps every batch on the
-// weight-streaming kernels).
+// weight type: 4 samples for F32 convolutions, 5 for BF16, where streaming half the bytes keeps
+// the sliced batch-1 kernels ahead one sample longer; measured crossovers: pusht B=4 7.31 ms
+// sliced against 6.32 on the matrix cores, bimanual B=4 3.91 against 4.48 and B=6 5.33 against
+// 4.56; a value above the max batch keeps every batch on the weight-streaming kernels).
 std::size_t env_mfma_batch() {
   const char* v = std::getenv("FLOWEDGE_MFMA_BATCH");
   if (v == nullptr || *v == '\0') return 0;
@@ -2137,7 +2138,7 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   e->arena_bytes = work_base + e->w.size;
   // Measured crossovers (DDIM-10 ticks): the fused weight-streaming kernels stay faster through
   // 4 samples with F32 weights and 7 with BF16 weights.
-  if (e->mfma_batch == 0) e->mfma_batch = e->bf16_convs ? 8 : 5;
+  if (e->mfma_batch == 0) e->mfma_batch = e->bf16_convs ? 5 : 4;
 
   int count = 0;
   hipError_t st = hipGetDeviceCount(&count);

@@ -100,7 +100,7 @@ def test_general_shape_bf16_weights(ckpt_dir):
     spec = dataclasses.replace(unet_ref.GENERAL_SPECS["k7_h6_g3"], bf16_weights=True)
     path = unet_ref.write_variant(os.path.join(ckpt_dir, "general_k7_bf16.safetensors"), spec)
     o = oracle.Oracle(path)
-    B = 9  # above the BF16 matrix-core threshold (8)
+    B = 9  # above the BF16 matrix-core threshold (5)
     cond, noise = ck.inputs(spec, batch=B)
     say("general k7 h6 BF16 weights, batch 1 and 9")
     with flowedge_amd.Engine(path) as e:

@@ -4,7 +4,7 @@ Tolerances (written per test): fp32 checkpoints must match within max |err| <= 1
 units (action scale (max - min)/2 = 1 for the synthetic range [-1, 1]); BF16-weight checkpoints
 are held to the same 1e-4 here because the oracle runs on the identical BF16-rounded values
 (the contract bound for BF16 variants is 2e-2).  Batches below the matrix-core threshold
-(FLOWEDGE_MFMA_BATCH, default 5 for F32 weights and 8 for BF16) run the batch-1 kernels and must
+(FLOWEDGE_MFMA_BATCH, default 4 for F32 weights and 5 for BF16) run the batch-1 kernels and must
 equal independent batch-1 calls bit for bit; larger batches run implicit GEMMs on the matrix
 cores (another summation order) and are held to the oracle per sample at the same 1e-4.
 """
@@ -290,16 +290,16 @@ def test_pusht_kernel_paths(pusht):
         names = [c["name"] for c in e.convolutions()]
         assert len(names) == 29
         assert e.conv_paths(1) == ["fused"] * 29
-        assert e.conv_paths(4) == ["fused"] * 29
-        assert e.conv_paths(5) == ["matrix"] * 29
+        assert e.conv_paths(3) == ["fused"] * 29
+        assert e.conv_paths(4) == ["matrix"] * 29
         assert e.conv_paths(256) == ["matrix"] * 29
         # Below the matrix-core threshold every convolution but the first (2 input channels) runs
         # with its input channels split into 8 slices.  On the matrix cores, small batches leave
         # the partial sums of a split K loop (at most 8) for the consumer to add; at 256 samples
         # the output tiles fill the GPU and nothing is split.
         assert e.conv_slices(1) == [1] + [8] * 28
-        assert e.conv_slices(4) == [1] + [8] * 28
-        parts = e.conv_slices(5)
+        assert e.conv_slices(3) == [1] + [8] * 28
+        parts = e.conv_slices(4)
         assert all(1 <= p <= 8 for p in parts) and max(parts) > 1, parts
         assert e.conv_slices(256) == [1] * 29
 
