@@ -38,6 +38,8 @@ using namespace mm;
 constexpr int kKC = 16;   // input channels per K step
 constexpr int kPad = 4;   // LDS row padding (floats)
 
+__host__ __device__ constexpr int mm_threads(int nt) { return nt >= 128 ? 512 : kMmThreads; }
+
 // KS: input channels per K step, kKC (narrow inputs, double-buffered weights) or 2 kKC (one
 // weight buffer, refilled after a barrier: half the per-step staging chains).
 template <int MODE, int K, int LIN, int MT, int NT, int KS = kKC>
@@ -52,14 +54,18 @@ struct MmShape {
   static constexpr int XROWS = SB * LIN + 1;
   static constexpr int WFLOATS = MT * WROW;
   static constexpr int XFLOATS = XROWS * XROW;
-  static constexpr int UW = MT * K * (KS / 4) / kMmThreads;  // weight float4 per lane per step
+  // 64 x 128 tiles take eight wavefronts (two per SIMD, so one wavefront's LDS reads overlap
+  // another's MFMAs) in a 2 x 4 grid of 32 x 32 tiles; smaller tiles four in a 2 x 2 grid.
+  static constexpr int THREADS = mm_threads(NT);
+  static constexpr int WAVE_COLS = THREADS / 64 / 2;
+  static constexpr int UW = MT * K * (KS / 4) / THREADS;  // weight float4 per lane per step
   static constexpr int XELEMS = SB * KS * LIN;               // input floats per step
   static constexpr int XV = LIN >= 4 ? 4 : 1;          // vector width of input loads
   static constexpr int XUNITS = XELEMS / XV;
-  static constexpr int UX = (XUNITS + kMmThreads - 1) / kMmThreads;
-  static constexpr int WM = MT / 2, WN = NT / 2;
+  static constexpr int UX = (XUNITS + THREADS - 1) / THREADS;
+  static constexpr int WM = MT / 2, WN = NT / WAVE_COLS;
   static constexpr int TI = WM / 16, TJ = WN / 16;
-  static_assert(MT * K * (KS / 4) % kMmThreads == 0, "weight units per lane");
+  static_assert(MT * K * (KS / 4) % THREADS == 0, "weight units per lane");
   static constexpr std::size_t LDS_FLOATS = WBUF * WFLOATS + 2 * XFLOATS;
   static_assert(NT % LOUT == 0 && XELEMS % XV == 0, "column tile");
 };
@@ -76,7 +82,7 @@ __device__ __forceinline__ float4 load_w4(const void* base, std::int64_t idx) {
 }
 
 template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
-__global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
+__global__ __launch_bounds__(mm_threads(NT)) void conv_mfma_kernel(MmArgs a) {
   using S = MmShape<MODE, K, LIN, MT, NT, NARROW ? kKC : 2 * kKC>;
   constexpr int KS = NARROW ? kKC : 2 * kKC;
   extern __shared__ float4 lds4[];
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     const int ic0 = step * KS;
 #pragma unroll
     for (int r = 0; r < S::UW; ++r) {
-      const int u = tid + r * kMmThreads;
+      const int u = tid + r * S::THREADS;
       const int m = u / (K * (KS / 4)), rem = u - m * (K * (KS / 4));
       const int k = rem / (KS / 4), q = rem % (KS / 4);
       const int oc = m0 + m;
@@ -134,7 +140,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < S::UX; ++r) {
-      const int u = tid + r * kMmThreads;
+      const int u = tid + r * S::THREADS;
       if constexpr (S::XV == 4) {
         const int bl = u / (KS / 4 * LIN), v = u - bl * (KS / 4 * LIN);
         const int ch = v / (LIN / 4), t4 = (v - ch * (LIN / 4)) * 4;
@@ -164,14 +170,14 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     float* X = Xs + buf * S::XFLOATS;
 #pragma unroll
     for (int r = 0; r < S::UW; ++r) {
-      const int u = tid + r * kMmThreads;
+      const int u = tid + r * S::THREADS;
       const int m = u / (K * (KS / 4)), rem = u - m * (K * (KS / 4));
       const int k = rem / (KS / 4), q = rem % (KS / 4);
       *reinterpret_cast<float4*>(W + m * S::WROW + k * KS + 4 * q) = wreg[r];
     }
 #pragma unroll
     for (int r = 0; r < S::UX; ++r) {
-      const int u = tid + r * kMmThreads;
+      const int u = tid + r * S::THREADS;
       if (u >= S::XUNITS) continue;
       if constexpr (S::XV == 4) {
         const int bl = u / (KS / 4 * LIN), v = u - bl * (KS / 4 * LIN);
@@ -193,7 +199,8 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
   // ConvTranspose the columns are in parity order, so wavefront column half wc holds output
   // positions of parity wc only, which taps of the other parity never reach.
   constexpr int PAR = MODE == kConvTranspose ? 1 : 0;
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave / S::WAVE_COLS, wc = wave % S::WAVE_COLS;
+  const int par = 2 * wc / S::WAVE_COLS;  // output parity of this wavefront's columns (PAR)
   const int kq = lane >> 4, l16 = lane & 15;
   int xrow[S::TJ][K];
 #pragma unroll
@@ -225,9 +232,9 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     const float* X = Xs + buf * S::XFLOATS;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      // Output t takes tap k when t + 1 - k is even: parity wc takes the taps k = wc + 1 mod 2.
+      // Output t takes tap k when t + 1 - k is even: parity par takes the taps k = par + 1 mod 2.
       if constexpr (PAR) {
-        if (((k + wc + 1) & 1) != 0) continue;
+        if (((k + par + 1) & 1) != 0) continue;
       }
 #pragma unroll
       for (int kc = 0; kc < KS / kKC; ++kc) {
@@ -289,7 +296,7 @@ __global__ __launch_bounds__(kMmThreads) void conv_mfma_kernel(MmArgs a) {
     }
     __syncthreads();
     float* yk = a.y + ks * a.ypart;
-    for (int idx = tid; idx < NT * MT; idx += kMmThreads) {
+    for (int idx = tid; idx < NT * MT; idx += S::THREADS) {
       const int bl = idx / (MT * S::LOUT);
       const int rem = idx - bl * (MT * S::LOUT);
       const int row = rem / S::LOUT, t = rem - row * S::LOUT;
@@ -434,7 +441,7 @@ hipError_t launch_mm(const MmArgs& a, hipStream_t s) {
     if (st != hipSuccess) return st;
     raised = true;
   }
-  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles * a.ksplit), dim3(kMmThreads), smem, s, a);
+  hipLaunchKernelGGL(fn, dim3(a.mtiles * a.ntiles * a.ksplit), dim3(S::THREADS), smem, s, a);
   return hipGetLastError();
 }
 
