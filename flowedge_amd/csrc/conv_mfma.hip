@@ -46,7 +46,10 @@ template <int MODE, int K, int LIN, int MT, int NT, int KS = kKC>
 struct MmShape {
   static constexpr int LOUT = lout_for(MODE, LIN);
   static constexpr int SB = NT / LOUT;           // samples per column tile
-  static constexpr bool W1 = KS > kKC;           // one weight buffer in LDS
+  // One weight buffer in LDS (two workgroups per CU) for 32-channel steps on 64 x 64 and
+  // 64 x 32 tiles; 64 x 128 tiles (one eight-wavefront workgroup per CU at the batches that
+  // choose them) keep two and skip the refill barrier: pusht B=256 54.3 -> 53.9 ms.
+  static constexpr bool W1 = KS > kKC && NT < 128;
   static constexpr int WBUF = W1 ? 1 : 2;
   static constexpr int WROW = K * KS + kPad;     // LDS floats per weight row
   static constexpr int XROW = KS + kPad;         // LDS floats per (sample, position) row
