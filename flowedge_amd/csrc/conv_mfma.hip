@@ -38,7 +38,9 @@ using namespace mm;
 constexpr int kKC = 16;   // input channels per K step
 constexpr int kPad = 4;   // LDS row padding (floats)
 
-__host__ __device__ constexpr int mm_threads(int nt) { return nt >= 128 ? 512 : kMmThreads; }
+__host__ __device__ constexpr int mm_threads(int nt, int ks) {
+  return nt >= 128 || (nt >= 64 && ks > kKC) ? 512 : kMmThreads;
+}
 
 // KS: input channels per K step, kKC (narrow inputs, double-buffered weights) or 2 kKC (one
 // weight buffer, refilled after a barrier: half the per-step staging chains).
@@ -57,9 +59,10 @@ struct MmShape {
   static constexpr int XROWS = SB * LIN + 1;
   static constexpr int WFLOATS = MT * WROW;
   static constexpr int XFLOATS = XROWS * XROW;
-  // 64 x 128 tiles take eight wavefronts (two per SIMD, so one wavefront's LDS reads overlap
-  // another's MFMAs) in a 2 x 4 grid of 32 x 32 tiles; smaller tiles four in a 2 x 2 grid.
-  static constexpr int THREADS = mm_threads(NT);
+  // 64 x 128 and (32-channel steps) 64 x 64 tiles take eight wavefronts, two per SIMD, so one
+  // wavefront's LDS reads overlap another's MFMAs (a 2 x 4 grid of 32 x 32 or 32 x 16 tiles);
+  // 64 x 32 and narrow 64 x 64 tiles four in a 2 x 2 grid.
+  static constexpr int THREADS = mm_threads(NT, KS);
   static constexpr int WAVE_COLS = THREADS / 64 / 2;
   static constexpr int UW = MT * K * (KS / 4) / THREADS;  // weight float4 per lane per step
   static constexpr int XELEMS = SB * KS * LIN;               // input floats per step
@@ -85,7 +88,8 @@ __device__ __forceinline__ float4 load_w4(const void* base, std::int64_t idx) {
 }
 
 template <int MODE, int K, int LIN, bool BF16, int MT, int NT, bool NARROW>
-__global__ __launch_bounds__(mm_threads(NT)) void conv_mfma_kernel(MmArgs a) {
+__global__ __launch_bounds__(mm_threads(NT, NARROW ? kKC : 2 * kKC))
+void conv_mfma_kernel(MmArgs a) {
   using S = MmShape<MODE, K, LIN, MT, NT, NARROW ? kKC : 2 * kKC>;
   constexpr int KS = NARROW ? kKC : 2 * kKC;
   extern __shared__ float4 lds4[];
