@@ -112,6 +112,12 @@ void conv_mfma_kernel(MmArgs a) {
   const int nall = (a.ic + KS - 1) / KS;
   const int s0 = ks * nall / a.ksplit, s1 = (ks + 1) * nall / a.ksplit;
 
+  // The bias of the tile's rows (first K slice only), read before the first K step's loads
+  // and kept in LDS for the epilogue.
+  __shared__ float bias_t[MT];
+  float bias_r = 0.0f;
+  if (tid < MT && ks == 0 && m0 + tid < a.oc) bias_r = a.bias[m0 + tid];
+
   // Zero rows of both input buffers (never overwritten).
   if (tid < 2 * KS) Xs[(tid / KS) * S::XFLOATS + S::ZERO * S::XROW + (tid % KS)] = 0.0f;
 
@@ -230,6 +236,7 @@ void conv_mfma_kernel(MmArgs a) {
     for (int j = 0; j < S::TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   load_step(s0);
+  if (tid < MT) bias_t[tid] = bias_r;
   store_step(0);
   __syncthreads();
   for (int step = s0; step < s1; ++step) {
@@ -310,7 +317,7 @@ void conv_mfma_kernel(MmArgs a) {
       const int b = b0 + bl, oc = m0 + row;
       if (b < a.batch && oc < a.oc)
         yk[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
-            T[(bl * S::LOUT + t) * TROW + row] + (ks == 0 ? a.bias[oc] : 0.0f);
+            T[(bl * S::LOUT + t) * TROW + row] + bias_t[row];
     }
   } else {
 #pragma unroll
@@ -319,7 +326,7 @@ void conv_mfma_kernel(MmArgs a) {
       for (int e = 0; e < 4; ++e) {
         const int oc = m0 + wr * S::WM + 16 * i + 4 * kq + e;
         if (oc >= a.oc) continue;
-        const float bias = ks == 0 ? a.bias[oc] : 0.0f;
+        const float bias = bias_t[wr * S::WM + 16 * i + 4 * kq + e];
 #pragma unroll
         for (int j = 0; j < S::TJ; ++j) {
           const int col = wc * S::WN + 16 * j + l16;

@@ -117,6 +117,12 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   const int nall = a.ic / S::KS;
   const int s0 = ks * nall / a.ksplit, s1 = (ks + 1) * nall / a.ksplit;
 
+  // The bias of the tile's rows (first K slice only), read before the first K step's loads
+  // and kept in LDS for the epilogue.
+  __shared__ float bias_t[MT];
+  float bias_r = 0.0f;
+  if (tid < MT && ks == 0 && m0 + tid < a.oc) bias_r = a.bias[m0 + tid];
+
   // Zero rows of both input buffers (never overwritten).
   if (tid < 2 * S::KS) {
     const int buf = tid / S::KS, c = tid % S::KS;
@@ -323,6 +329,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
   // 20.8 us for the 2048<-2048 L2 layer.)
   Regs rn;
   load_step(s0, rn);
+  if (tid < MT) bias_t[tid] = bias_r;
   store_step(0, rn);
   __syncthreads();
   for (int step = s0; step < s1; ++step) {
@@ -374,7 +381,7 @@ __global__ __launch_bounds__(threads_for(NT)) void conv_mfma_bf16_kernel(MmArgs 
     const int b = b0 + bl2, oc = m0 + row;
     if (b < a.batch && oc < a.oc)
       yk[b * a.ys + static_cast<std::int64_t>(oc) * S::LOUT + t] =
-          T[(bl2 * S::LOUT + t) * TROW + row] + (ks == 0 ? a.bias[oc] : 0.0f);
+          T[(bl2 * S::LOUT + t) * TROW + row] + bias_t[row];
   }
 }
 
