@@ -733,6 +733,12 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
   auto do_tile = [&](int tile, auto refill) {
     const int row = tile * rpt + gid;
     const int nrow = (tile + a.blocks) * rpt + gid;
+    // The row's biases (added by slice 0 only), read before the products so that their latency
+    // hides behind them instead of delaying the output stores.
+    const bool brow = row < a.oc && (!SL || sl == 0);
+    const float bv = brow ? a.bias[row] : 0.0f;
+    float rbv = 0.0f;
+    if constexpr (RES) rbv = brow ? a.rbias[row] : 0.0f;
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
@@ -808,10 +814,10 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
       if (rs_writer_seg<V, STPR>(lane) && row < a.oc) {
         if (!RES || off < LOUT)
           put(a.y + b * a.ys + sl * a.ypart + static_cast<std::int64_t>(row) * LOUT + off,
-              sl == 0 ? acc[0] + a.bias[row] : acc[0]);
+              sl == 0 ? acc[0] + bv : acc[0]);
         else
           put(a.yr + b * a.yrs + sl * a.yrpart + static_cast<std::int64_t>(row) * LOUT + off - LOUT,
-              sl == 0 ? acc[0] + a.rbias[row] : acc[0]);
+              sl == 0 ? acc[0] + rbv : acc[0]);
       }
       return;
     }
@@ -820,10 +826,10 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
     if (waves == 1) {
       if (rs_writer<V>(lane) && row < a.oc) {
         if (!RES || off < LOUT)
-          put(a.y + b * a.ys + static_cast<std::int64_t>(row) * LOUT + off, acc[0] + a.bias[row]);
+          put(a.y + b * a.ys + static_cast<std::int64_t>(row) * LOUT + off, acc[0] + bv);
         else
           put(a.yr + b * a.yrs + static_cast<std::int64_t>(row) * LOUT + off - LOUT,
-              acc[0] + a.rbias[row]);
+              acc[0] + rbv);
       }
       return;
     }
@@ -837,10 +843,10 @@ __device__ __forceinline__ bool conv_body(const Args& a, int wg, int b, float* x
       float sum = 0.0f;
       for (int wv = 0; wv < waves; ++wv) sum += gred[wv * V + lg];
       if (!RES || lg < LOUT)
-        put(a.y + b * a.ys + static_cast<std::int64_t>(row) * LOUT + lg, sum + a.bias[row]);
+        put(a.y + b * a.ys + static_cast<std::int64_t>(row) * LOUT + lg, sum + bv);
       else
         put(a.yr + b * a.yrs + static_cast<std::int64_t>(row) * LOUT + lg - LOUT,
-            sum + a.rbias[row]);
+            sum + rbv);
     }
   };
   for (; tile + a.blocks < a.tiles; tile += a.blocks) do_tile(tile, std::true_type{});
