@@ -216,6 +216,7 @@ struct Work {
   std::size_t final_in = 0, fconv_out = 0;  // [B][dims0][H]
   std::size_t xnorm = 0;   // batched path: normalised input of one convolution
   std::size_t splitk = 0;  // batched path: split-K partial tiles
+  std::size_t upd_part = 0;  // split update: per-group partial outputs [B][8][A][H]
 };
 
 struct GraphEntry {
@@ -247,6 +248,10 @@ struct FeEngine {
   std::size_t arena_bytes = 0;
   char* ws = nullptr;  // workspace base of `w`
   Work w;
+  // The engine's own workspace base, and the split update's per-sample arrival counters (after
+  // the workspace in the arena; zeroed at load, left at zero by every split update launch).
+  char* own_ws = nullptr;
+  unsigned* upd_done = nullptr;
   // This device's static scratch array (allocation-free entry point), set up at load.
   void* scratch = nullptr;
   hipError_t scratch_status = hipErrorNotInitialized;
@@ -623,6 +628,7 @@ Work plan_work(const FeEngine& e, std::size_t batch, std::size_t rows, std::size
     norm_floats = std::max(norm_floats, c.dims[st] * (c.horizon >> st));
   w.xnorm = plan.take(B * norm_floats * 4);
   w.splitk = plan.take(splitk_floats * 4);
+  w.upd_part = plan.take(B * kFinalNormGroups * v * 4);
   w.size = plan.size;
   return w;
 }
@@ -1125,6 +1131,11 @@ void update_base(const FeEngine& e, fe::hip::UpdateOp& upd) {
   upd.groups = static_cast<int>(kFinalNormGroups);
   upd.wo = static_cast<const float*>(e.fout.op.w);
   upd.bo = e.fout.op.b;
+  // The split update keeps its counters in the engine's arena: only on the engine's workspace.
+  if (e.upd_done != nullptr && e.ws == e.own_ws) {
+    upd.done = e.upd_done;
+    upd.epart = e.wp(e.w.upd_part);
+  }
 }
 
 // One U-Net evaluation on xin (FiLM time row `film_row`), ending with `upd`
@@ -2006,6 +2017,12 @@ bool side_streams() {
   return v == nullptr || std::strcmp(v, "0") != 0;
 }
 
+// FLOWEDGE_SPLIT_UPDATE=0 keeps the final update on one workgroup per sample.
+bool split_update() {
+  const char* v = std::getenv("FLOWEDGE_SPLIT_UPDATE");
+  return v == nullptr || std::strcmp(v, "0") != 0;
+}
+
 std::size_t env_max_batch() {
   const char* v = std::getenv("FLOWEDGE_MAX_BATCH");
   if (v == nullptr || *v == '\0') return 256;
@@ -2135,7 +2152,8 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   }
   const std::size_t work_base = (builder.plan.size + kAlign - 1) / kAlign * kAlign;
   e->w = plan_work(*e, e->max_batch, e->max_nfe, kSplitKFloats);
-  e->arena_bytes = work_base + e->w.size;
+  const std::size_t done_off = work_base + (e->w.size + kAlign - 1) / kAlign * kAlign;
+  e->arena_bytes = done_off + e->max_batch * sizeof(unsigned);
   // Measured crossovers (DDIM-10 ticks): the fused weight-streaming kernels stay faster through
   // 4 samples with F32 weights and 7 with BF16 weights.
   if (e->mfma_batch == 0) e->mfma_batch = e->bf16_convs ? 5 : 4;
@@ -2165,6 +2183,14 @@ fe_engine* create_engine(std::shared_ptr<const fe::Checkpoint> ck, unsigned thre
   }
   g_device_allocs.fetch_add(1);
   e->ws = e->arena + work_base;
+  e->own_ws = e->ws;
+  if (split_update()) {
+    e->upd_done = reinterpret_cast<unsigned*>(e->arena + done_off);
+    if ((st = hipMemset(e->upd_done, 0, e->max_batch * sizeof(unsigned))) != hipSuccess) {
+      hip_fail("Device arena initialisation failed", st);
+      return nullptr;
+    }
+  }
   const std::size_t B = e->max_batch, nv = B * e->values, nc = B * e->cfg.cond_dim;
   const std::size_t pin_bytes = (nc + 2 * nv) * 4 + 64;
   void* pin = nullptr;

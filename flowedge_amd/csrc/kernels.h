@@ -224,6 +224,10 @@ struct UpdateOp {
   std::uint64_t noise_offset = 0;       // Gaussian stream index of this step's first value
   int add_noise = 0;
   float dt = 0;
+  // Split update (512 final channels in 8 groups): per-sample arrival counters, zero between
+  // launches, and the per-group partial outputs [B][8][A][H].  Null: one workgroup per sample.
+  unsigned* done = nullptr;
+  float* epart = nullptr;
 };
 // One block per sample.  Shapes outside the fused kernel's instances (horizon not a power of two
 // up to 16, c0 > 1024, more than 64 actions or 32 groups) run on a general kernel (one wavefront

@@ -163,6 +163,119 @@ __global__ __launch_bounds__(upd::kUpdThreads) void update_kernel(UpdateOp op) {
   upd::update_body<H, false, CPL>(op, blockIdx.x, gridDim.x, sm);
 }
 
+// update_kernel<H, 1> split over the groups of a 512-channel final width in 8 groups of 64: one
+// wavefront per (sample, group), so the final convolution's partial sums are read by eight CUs
+// instead of one.  Wavefront g does what wavefront g of update_kernel does (its group's
+// statistics, GroupNorm + Mish, and the 1x1 conv's partial sums over the group's 64 channels,
+// reduced in the same order) and stores them device-coherently in op.epart; the sample's last
+// wavefront to arrive (op.done counts arrivals; that wavefront resets it) adds the eight partials
+// in group order, as update_kernel adds its wavefronts' partials, and runs the sampler update.
+// Results are bit-identical to update_kernel's.
+constexpr int kSplitGroups = 8;
+constexpr int kSplitChannels = kSplitGroups * kWave;
+// Up to this batch (128 wavefronts): pusht B=1 tick 2.716 -> 2.683 ms; at 64 samples the
+// one-workgroup form is ahead (bimanual B=64 5.45 against 5.48 ms).
+constexpr int kSplitMaxBatch = 16;
+
+template <int H>
+__global__ __launch_bounds__(kWave) void update_split_kernel(UpdateOp op) {
+  constexpr int AG = H >= kWave ? 1 : kWave / H;  // actions per reduction pass
+  constexpr int V = AG * H;
+  constexpr int PM = upd::kMaxUpdateParts;
+  const int b = blockIdx.x / kSplitGroups, g = blockIdx.x % kSplitGroups;
+  const int lane = threadIdx.x;
+  const int A = op.action_dim, C = kSplitChannels;
+  const int c = g * kWave + lane;
+  const std::int64_t sample = static_cast<std::int64_t>(b) * A * H;
+  const float* p = op.h + b * (op.hstride != 0 ? op.hstride : static_cast<std::int64_t>(C) * H) +
+                   static_cast<std::int64_t>(c) * H;
+  float w0[AG];
+#pragma unroll
+  for (int aa = 0; aa < AG; ++aa)
+    w0[aa] = aa < A ? op.wo[static_cast<std::int64_t>(aa) * C + c] : 0.0f;
+  const float gam = op.gamma[c], bet = op.beta[c];
+  float pv[PM][H];
+#pragma unroll
+  for (int j = 0; j < PM; ++j) {
+    const float* pj = p + j * op.hpart;
+    const bool on = j < op.hparts;
+    if constexpr (H >= 4) {
+#pragma unroll
+      for (int t = 0; t < H; t += 4) {
+        const float4 v = on ? *reinterpret_cast<const float4*>(pj + t) : float4{0, 0, 0, 0};
+        pv[j][t] = v.x;
+        pv[j][t + 1] = v.y;
+        pv[j][t + 2] = v.z;
+        pv[j][t + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < H; ++t) pv[j][t] = on ? pj[t] : 0.0f;
+    }
+  }
+  float hv[H];
+  double s = 0.0, q = 0.0;
+#pragma unroll
+  for (int t = 0; t < H; ++t) {
+    float v = pv[0][t];
+#pragma unroll
+    for (int j = 1; j < PM; ++j)
+      if (j < op.hparts) v += pv[j][t];
+    hv[t] = v;
+    const double d = static_cast<double>(v);
+    s += d;
+    q += d * d;
+  }
+  double gs = 0.0, gq = 0.0;
+  gs += s;
+  gq += q;
+  gs = wave_sum(gs);
+  gq = wave_sum(gq);
+  const double n = static_cast<double>(kWave) * H;
+  const double mean = gs / n;
+  const double var = fmax(0.0, gq / n - mean * mean);
+  const float meanf = static_cast<float>(mean);
+  const float inv = static_cast<float>(1.0 / sqrt(var + 1e-5));
+  const float scale = inv * gam;
+#pragma unroll
+  for (int t = 0; t < H; ++t) hv[t] = mish_fast(fmaf(hv[t] - meanf, scale, bet));
+  float* ep = op.epart + (static_cast<std::int64_t>(b) * kSplitGroups + g) * A * H;
+  for (int a0 = 0; a0 < A; a0 += AG) {
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int aa = 0; aa < AG; ++aa) {
+      const int a = a0 + aa;
+      const float w = a0 == 0 ? w0[aa]
+                              : (a < A ? op.wo[static_cast<std::int64_t>(a) * C + c] : 0.0f);
+#pragma unroll
+      for (int t = 0; t < H; ++t) acc[aa * H + t] = fmaf(w, hv[t], acc[aa * H + t]);
+    }
+    rs_step<V, 32>(acc, lane);
+    const int off = rs_offset<V>(lane);
+    if (rs_writer<V>(lane) && a0 * H + off < A * H) st_dev(ep + a0 * H + off, acc[0]);
+  }
+  // Publish once the partials have reached the device's coherence point.
+  wait_vmem();
+  unsigned before = 0;
+  if (lane == 0)
+    before = __hip_atomic_fetch_add(global_ptr(op.done + b), 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  before = __builtin_amdgcn_readfirstlane(before);
+  if (before != kSplitGroups - 1) return;
+  if (lane == 0) st_dev(op.done + b, 0u);
+  const float* e0 = op.epart + static_cast<std::int64_t>(b) * kSplitGroups * A * H;
+  for (int i = lane; i < A * H; i += kWave) {
+    float e = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < kSplitGroups; ++gg) e += ld_dev(e0 + gg * A * H + i);
+    const int a = i / H, t = i % H;
+    const float xv = op.kind != kUpdateDenoise ? op.x[sample + i] : 0.0f;
+    upd::apply_update<false>(op, sample, gridDim.x / kSplitGroups, a, t, A, H, e + op.bo[a], xv);
+  }
+}
+
 // Shapes outside update_kernel's instances: one wavefront per output value eps[a][t] (lanes
 // stride the c0 channels), the group statistics first (fp64, one wavefront per group).
 constexpr int kUpdGenThreads = 256;
@@ -287,6 +400,18 @@ hipError_t update(const UpdateOp& op, int batch, hipStream_t stream) {
     return hipErrorInvalidValue;
   if (!update_fused_ok(op.c0, op.groups, op.horizon, op.action_dim)) {
     hipLaunchKernelGGL(update_general_kernel, dim3(batch), dim3(kUpdGenThreads), 0, stream, op);
+    return hipGetLastError();
+  }
+  if (op.done != nullptr && op.epart != nullptr && op.c0 == kSplitChannels &&
+      op.groups == kSplitGroups && op.horizon <= kWave && batch <= kSplitMaxBatch) {
+    const dim3 grid(static_cast<unsigned>(batch * kSplitGroups));
+    switch (op.horizon) {
+      case 1: hipLaunchKernelGGL(update_split_kernel<1>, grid, dim3(kWave), 0, stream, op); break;
+      case 2: hipLaunchKernelGGL(update_split_kernel<2>, grid, dim3(kWave), 0, stream, op); break;
+      case 4: hipLaunchKernelGGL(update_split_kernel<4>, grid, dim3(kWave), 0, stream, op); break;
+      case 8: hipLaunchKernelGGL(update_split_kernel<8>, grid, dim3(kWave), 0, stream, op); break;
+      default: hipLaunchKernelGGL(update_split_kernel<16>, grid, dim3(kWave), 0, stream, op); break;
+    }
     return hipGetLastError();
   }
   if (op.c0 <= upd::kUpdThreads) {

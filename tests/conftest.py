@@ -20,3 +20,20 @@ def ckpt_dir(tmp_path_factory):
         os.makedirs(d, exist_ok=True)
         return d
     return str(tmp_path_factory.mktemp("ckpt"))
+
+
+@pytest.fixture(scope="session", autouse=True)
+def torch_gpu_first(request):
+    """Initialises torch's GPU runtime before any engine exists in a session that runs GPU tests.
+
+    torch (ROCm wheel) fails its first GPU initialisation with "No HIP GPUs are available" when
+    it happens after an engine of this library was created and freed in the same process and
+    none is alive; initialised earlier, it keeps working.  GPU tests that hand device tensors to
+    the C ABI therefore do not depend on which test touched torch's GPU first.
+    """
+    if any(item.get_closest_marker("gpu") for item in request.session.items):
+        import torch
+
+        if torch.cuda.is_available():
+            torch.cuda.init()
+    yield
