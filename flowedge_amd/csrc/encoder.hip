@@ -334,6 +334,18 @@ __global__ __launch_bounds__(kNormThreads) void enc_norm_fused_kernel(NormArgs a
       rv[r] = i < n ? rp[i] : 0.0f;
     }
   }
+  // The affine coefficients of each value's channel are read with the values, before the
+  // statistics, so that their latency is not added after them.
+  float ga[R], be[R], rga[R], rbe[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid + r * kNormThreads;
+    const int c = g * cpg + (i < n ? i / hw : 0);
+    ga[r] = a.gamma[c];
+    be[r] = a.beta[c];
+    rga[r] = a.mode == kNormEndGn ? a.rgamma[c] : 0.0f;
+    rbe[r] = a.mode == kNormEndGn ? a.rbeta[c] : 0.0f;
+  }
   double s = 0.0, q = 0.0;
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -362,10 +374,9 @@ __global__ __launch_bounds__(kNormThreads) void enc_norm_fused_kernel(NormArgs a
   for (int r = 0; r < R; ++r) {
     const int i = tid + r * kNormThreads;
     if (i >= n) continue;
-    const int c = g * cpg + i / hw;
-    float o = fmaf(v[r] - mean, inv * a.gamma[c], a.beta[c]);
+    float o = fmaf(v[r] - mean, inv * ga[r], be[r]);
     if (a.mode == kNormEndPlain) o += rv[r];
-    if (a.mode == kNormEndGn) o += fmaf(rv[r] - rmean, rinv * a.rgamma[c], a.rbeta[c]);
+    if (a.mode == kNormEndGn) o += fmaf(rv[r] - rmean, rinv * rga[r], rbe[r]);
     out[i] = fmaxf(o, 0.0f);
   }
 }
