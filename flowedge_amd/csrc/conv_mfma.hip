@@ -378,6 +378,25 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
   const int nqn = in.split * LIN / 4;
   const int npg = in.split / in.groups * LIN / 4;
   const float* src = in.src + b * in.src_stride;
+  const float* ft = in.film_time != nullptr ? in.film_time + in.film_off : nullptr;
+  const float* fc = in.film_time != nullptr ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
+  // LIN >= 4: one channel per 16-byte group, whose affine and FiLM coefficients are read with the
+  // values, before the statistics, so that their latency is not added after them.
+  constexpr bool PRE = LIN >= 4;
+  float ga[QN], be[QN], t0[QN], c0[QN], t1[QN], c1[QN];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int m = 0; m < QN; ++m) {
+      const int q = tid + m * kNaThreads;
+      const int c = q < nqn ? 4 * q / LIN : 0;
+      ga[m] = in.gamma[c];
+      be[m] = in.beta[c];
+      t0[m] = ft != nullptr ? ft[c] : 0.0f;
+      c0[m] = ft != nullptr ? fc[c] : 0.0f;
+      t1[m] = ft != nullptr ? ft[in.split + c] : 0.0f;
+      c1[m] = ft != nullptr ? fc[in.split + c] : 0.0f;
+    }
+  }
   float4 x[QN], r[QN];
 #pragma unroll
   for (int m = 0; m < QN; ++m) {
@@ -421,8 +440,6 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
     }
   }
   __syncthreads();
-  const float* ft = in.film_time != nullptr ? in.film_time + in.film_off : nullptr;
-  const float* fc = in.film_time != nullptr ? in.film_cond + b * in.film_cond_stride + in.film_off : nullptr;
 #pragma unroll
   for (int m = 0; m < QN; ++m) {
     const int q = tid + m * kNaThreads;
@@ -433,9 +450,15 @@ __global__ __launch_bounds__(kNaThreads) void norm_act_kernel(ConvInput in, floa
     const float rr[4] = {r[m].x, r[m].y, r[m].z, r[m].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = (4 * q + i) / LIN;
-      float val = mish_fast(fmaf(v[i] - mean, inv * in.gamma[c], in.beta[c]));
-      if (ft != nullptr) val = fmaf(ft[c] + fc[c], val, ft[in.split + c] + fc[in.split + c]);
+      float val;
+      if constexpr (PRE) {
+        val = mish_fast(fmaf(v[i] - mean, inv * ga[m], be[m]));
+        if (ft != nullptr) val = fmaf(t0[m] + c0[m], val, t1[m] + c1[m]);
+      } else {
+        const int c = (4 * q + i) / LIN;
+        val = mish_fast(fmaf(v[i] - mean, inv * in.gamma[c], in.beta[c]));
+        if (ft != nullptr) val = fmaf(ft[c] + fc[c], val, ft[in.split + c] + fc[in.split + c]);
+      }
       v[i] = val + rr[i];
     }
     *reinterpret_cast<float4*>(dst + b * dst_stride + 4 * q) = float4{v[0], v[1], v[2], v[3]};
